@@ -1,0 +1,105 @@
+/*
+ * rk_paged_attention.h -- C ABI of the gfx950 (MI355X) paged-attention decode library.
+ *
+ * Library: librk_pa_gfx950.so (hand-written HIP for CDNA4, wave64).  No torch types cross
+ * this boundary: every tensor is a device pointer to a dense, contiguous buffer and every
+ * size is an int64_t.  All calls are asynchronous on the given HIP stream and never read
+ * device memory from the host, so they can be captured into a HIP graph.
+ *
+ * Reference interface each entry point replaces (zihaomu/radeon-kernels):
+ *   rk_pa_decode            -> benchmarks/paged_attention/native_paged_attention.hip:191-242
+ *                              (paged_attention_impl<W>, bound as attention_wave{1,4,8} at :244-283),
+ *                              reached from src/radeon_kernels/providers/native.py:25 with the
+ *                              arguments built at src/radeon_kernels/ops/paged_attention/api.py:117-124.
+ *   rk_pa_decode_workspace_bytes
+ *                           -> no reference counterpart: the reference kernel has no context split.
+ *                              The caller sizes the split-K partial buffer with it (the torch
+ *                              extension allocates it from the caching allocator).
+ *   rk_pa_last_error, rk_pa_version
+ *                           -> error text that TORCH_CHECK carried in the reference
+ *                              (native_paged_attention.hip:199-219,239-240).
+ *
+ * Tensor layouts (row-major, contiguous) -- identical to the reference contract
+ * (contracts/paged_attention_decode-1.0.json:5-14):
+ *   query           [batch, query_heads, head_dim]                      fp16 | bf16
+ *   key_cache       [num_blocks, block_size, kv_heads, head_dim]        fp16 | bf16
+ *   value_cache     [num_blocks, block_size, kv_heads, head_dim]        fp16 | bf16
+ *   block_tables    [batch, max_blocks_per_sequence]                    int32 | int64
+ *   context_lengths [batch]                                             int32 | int64
+ *   output          [batch, query_heads, head_dim]                      dtype of query
+ *
+ * Semantics (src/radeon_kernels/ops/paged_attention/reference.py:7-47): query head h reads KV head
+ * h / (query_heads / kv_heads); token t of sequence b lives in slot
+ * block_tables[b, t / block_size] * block_size + t % block_size; tokens t >= context_length are
+ * masked; softmax and both contractions accumulate in fp32; the result is rounded to the query
+ * dtype.  context_length is clamped to max_blocks_per_sequence * block_size; a context length
+ * <= 0 yields NaN (softmax over an empty set); tokens whose physical block id is outside
+ * [0, num_blocks) are skipped and never dereferenced.
+ */
+#ifndef RK_PAGED_ATTENTION_H
+#define RK_PAGED_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by every entry point. */
+#define RK_OK 0
+#define RK_ERR_INVALID_ARGUMENT 1 /* shapes, pointers or scalars violate the contract */
+#define RK_ERR_UNSUPPORTED 2      /* valid for the operator but not for this kernel */
+#define RK_ERR_WORKSPACE 3        /* workspace missing or smaller than required */
+#define RK_ERR_LAUNCH 4           /* the HIP runtime rejected a launch */
+
+/* Element types. */
+#define RK_DTYPE_FP16 0
+#define RK_DTYPE_BF16 1
+#define RK_INDEX_INT32 0
+#define RK_INDEX_INT64 1
+
+/* Kernel variants: how QK^T is computed (PV always runs on the vector ALUs). */
+#define RK_PA_VARIANT_MFMA 0 /* v_mfma_f32_16x16x32_{bf16,f16}, one 16-token tile per wave step */
+#define RK_PA_VARIANT_VALU 1 /* fp32 FMAs + DPP row reductions */
+
+/*
+ * Bytes of device workspace rk_pa_decode needs for this shape and partition size: split-K
+ * partial (max, sum, accumulator) records, fp32.  Zero when one partition covers
+ * max_blocks_per_sequence * block_size tokens (the single-pass launch needs none).
+ */
+int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t head_dim,
+                                 int64_t block_size, int64_t max_blocks_per_sequence,
+                                 int64_t partition_tokens, size_t* bytes);
+
+/*
+ * Paged-attention decode: one query token per sequence against the paged K/V cache.
+ *
+ * partition_tokens: context tokens per workgroup (split-K partition); a multiple of 64 in
+ *   [64, 8192] with partition_tokens / block_size <= 256.
+ * variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_VALU.
+ * workspace/workspace_bytes: device buffer of at least rk_pa_decode_workspace_bytes(...) bytes
+ *   (may be NULL/0 when that is zero).  Its contents need no initialisation.
+ * stream: hipStream_t to launch on (NULL = the null stream).
+ *
+ * Supported by this library: head_dim in {64, 128, 256}; block_size a power of two in
+ * [1, 256]; query_heads % kv_heads == 0; num_blocks < 2^31.
+ */
+int rk_pa_decode(const void* query, const void* key_cache, const void* value_cache,
+                 const void* block_tables, const void* context_lengths, void* output,
+                 void* workspace, size_t workspace_bytes, int64_t batch, int64_t query_heads,
+                 int64_t kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                 int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
+                 int64_t partition_tokens, int variant, void* stream);
+
+/* Text describing the last non-RK_OK status returned on the calling thread. */
+const char* rk_pa_last_error(void);
+
+/* Library version and target, e.g. "rk_pa_gfx950 1.0.0 (gfx950, wave64)". */
+const char* rk_pa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RK_PAGED_ATTENTION_H */

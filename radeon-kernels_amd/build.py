@@ -1,0 +1,216 @@
+"""Build the gfx950 paged-attention decode library and its repo-local kernel pack.
+
+Outputs (all under ``radeon-kernels_amd/packs/gfx950``):
+
+* ``lib/librk_pa_gfx950.so`` -- the C-ABI library (``include/rk_paged_attention.h``), HIP for gfx950.
+* ``lib/rk_pa_gfx950.so``    -- the PyTorch-ROCm binding (module ``rk_pa_gfx950``) that dispatch
+  entries load as a ``python_extension`` artifact.
+* ``manifest.json``          -- the kernel-pack manifest (same fields as the reference's
+  ``schemas/kernel-pack.schema.json``), stamped with the binding's SHA-256 and this environment.
+
+It also rewrites the winners' ``sha256`` and ``environment`` in
+``radeon_kernels/dispatch/paged_attention_decode-1.0.json`` from ``dispatch_plan.py``.  The
+reference binds every dispatch entry to the exact artifact digest and to the exact
+torch/Python/ROCm ABI (src/radeon_kernels/runtime/compatibility.py:94-102), so both files are
+generated after each build rather than written by hand.
+
+Run as ``python radeon-kernels_amd/build.py`` or through ``__graft_entry__.build()``.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import subprocess
+import sys
+import sysconfig
+import tempfile
+from pathlib import Path
+
+PACKAGE_ROOT = Path(__file__).resolve().parent
+REPO_ROOT = PACKAGE_ROOT.parent
+CSRC = PACKAGE_ROOT / "csrc"
+INCLUDE = REPO_ROOT / "include"
+PACK_DIR = PACKAGE_ROOT / "packs" / "gfx950"
+LIB_DIR = PACK_DIR / "lib"
+CABI_NAME = "librk_pa_gfx950.so"
+EXTENSION_NAME = "rk_pa_gfx950"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Packed-FP32 VALU ops stay disabled: all fp32 math uses the scalar VALU forms.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    f"-ffile-prefix-map={REPO_ROOT}=.",
+]
+
+
+def _hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    candidate = Path(rocm) / "bin" / "hipcc"
+    return str(candidate) if candidate.exists() else "hipcc"
+
+
+def _torch_paths() -> tuple[list[str], list[str]]:
+    from torch.utils import cpp_extension
+
+    try:
+        includes = list(cpp_extension.include_paths(device_type="cuda"))
+        libraries = list(cpp_extension.library_paths(device_type="cuda"))
+    except TypeError:  # older torch: boolean ``cuda`` argument
+        includes = list(cpp_extension.include_paths(True))
+        libraries = list(cpp_extension.library_paths(True))
+    rocm_include = str(Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "include")
+    if rocm_include not in includes:
+        includes.append(rocm_include)
+    return includes, libraries
+
+
+def _run(command: list[str], verbose: bool) -> subprocess.Popen:
+    if verbose:
+        print("+", " ".join(command), flush=True)
+    return subprocess.Popen(command, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def _finish(process: subprocess.Popen, what: str) -> None:
+    output, _ = process.communicate()
+    if process.returncode != 0:
+        raise RuntimeError(f"{what} failed (exit {process.returncode}):\n{output}")
+
+
+def _atomic_write(path: Path, text: str) -> None:
+    path.parent.mkdir(parents=True, exist_ok=True)
+    handle, temporary = tempfile.mkstemp(dir=path.parent, prefix=f".{path.name}.")
+    with os.fdopen(handle, "w", encoding="utf-8") as stream:
+        stream.write(text)
+    os.chmod(temporary, 0o644)
+    os.replace(temporary, path)
+
+
+def sha256_file(path: Path) -> str:
+    digest = hashlib.sha256()
+    with path.open("rb") as stream:
+        for chunk in iter(lambda: stream.read(1 << 20), b""):
+            digest.update(chunk)
+    return digest.hexdigest()
+
+
+def compile_libraries(verbose: bool = False) -> tuple[Path, Path]:
+    """Compile the C-ABI library (hipcc) and the torch binding (g++); return their paths."""
+
+    import torch  # noqa: F401  (paths and ABI flag come from the installed torch)
+
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    # A fixed build directory keeps the output byte-identical across builds: clang derives the
+    # offload compilation-unit id from the command line, which includes the output path.
+    work = PACKAGE_ROOT / "_build"
+    work.mkdir(exist_ok=True)
+    cabi_tmp = work / CABI_NAME
+    ext_obj = work / "pa_torch_ext.o"
+    ext_tmp = work / f"{EXTENSION_NAME}.so"
+
+    hip = _run(
+        [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(CSRC / "pa_decode_gfx950.hip"), "-o", str(cabi_tmp)],
+        verbose,
+    )
+    includes, libraries = _torch_paths()
+    import torch
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cxx = [
+        "g++",
+        "-O2",
+        "-std=c++17",
+        "-fPIC",
+        "-c",
+        "-D__HIP_PLATFORM_AMD__=1",
+        "-DUSE_ROCM=1",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        f"-DTORCH_EXTENSION_NAME={EXTENSION_NAME}",
+        "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-ffile-prefix-map={REPO_ROOT}=.",
+        *[f"-I{path}" for path in includes],
+        f"-I{sysconfig.get_paths()['include']}",
+        f"-I{INCLUDE}",
+        str(CSRC / "pa_torch_ext.cpp"),
+        "-o",
+        str(ext_obj),
+    ]
+    gxx = _run(cxx, verbose)
+    _finish(hip, "hipcc (C-ABI library)")
+    _finish(gxx, "g++ (torch binding)")
+    link = [
+        "g++",
+        "-shared",
+        str(ext_obj),
+        f"-L{work}",
+        *[f"-L{path}" for path in libraries],
+        "-l:" + CABI_NAME,
+        "-lc10",
+        "-lc10_hip",
+        "-ltorch",
+        "-ltorch_cpu",
+        "-ltorch_hip",
+        "-ltorch_python",
+        "-Wl,-rpath,$ORIGIN",
+        "-Wl,--build-id=none",
+        "-o",
+        str(ext_tmp),
+    ]
+    _finish(_run(link, verbose), "link (torch binding)")
+    os.replace(cabi_tmp, LIB_DIR / CABI_NAME)
+    os.replace(ext_tmp, LIB_DIR / f"{EXTENSION_NAME}.so")
+    ext_obj.unlink()
+    return LIB_DIR / CABI_NAME, LIB_DIR / f"{EXTENSION_NAME}.so"
+
+
+def environment_record() -> dict:
+    """Environment of the GPU this pack targets: gfx950 wave64 under the installed torch."""
+
+    import torch
+
+    sys.path.insert(0, str(PACKAGE_ROOT))
+    from radeon_kernels.runtime.fingerprint import normalize_rocm_abi
+
+    return {
+        "architecture": ARCH,
+        "wavefront_size": 64,
+        "rocm_abi": normalize_rocm_abi(str(torch.version.hip)),
+        "python_abi": f"cp{sys.version_info.major}{sys.version_info.minor}",
+        "pytorch_version": str(torch.__version__),
+    }
+
+
+def write_pack_and_dispatch(extension: Path) -> dict:
+    sys.path.insert(0, str(PACKAGE_ROOT))
+    from radeon_kernels.dispatch_plan import render_dispatch_manifest, render_pack_manifest
+
+    digest = sha256_file(extension)
+    environment = environment_record()
+    artifact = f"lib/{extension.name}"
+    pack = render_pack_manifest(environment=environment, artifact=artifact, sha256=digest)
+    _atomic_write(PACK_DIR / "manifest.json", json.dumps(pack, indent=2, sort_keys=True) + "\n")
+    dispatch = render_dispatch_manifest(environment=environment, artifact=artifact, sha256=digest)
+    target = PACKAGE_ROOT / "radeon_kernels" / "dispatch" / "paged_attention_decode-1.0.json"
+    _atomic_write(target, json.dumps(dispatch, indent=2, sort_keys=True) + "\n")
+    return {"sha256": digest, "environment": environment, "entries": len(dispatch["entries"])}
+
+
+def build(verbose: bool = False) -> dict:
+    _, extension = compile_libraries(verbose=verbose)
+    summary = write_pack_and_dispatch(extension)
+    if verbose:
+        print(json.dumps(summary, indent=2), flush=True)
+    return summary
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv or "--verbose" in sys.argv)

@@ -1,0 +1,747 @@
+// Paged-attention decode for MI355X (gfx950, CDNA4, wave64).
+//
+// Operator semantics follow the reference fallback
+// (src/radeon_kernels/ops/paged_attention/reference.py:7-47) and contract
+// (contracts/paged_attention_decode-1.0.json:15-25): one query token per sequence, query head h
+// reads KV head h / (Hq / Hkv), token t lives in slot block_tables[b, t / BS] * BS + t % BS,
+// tokens t >= context_length are masked, fp32 softmax and accumulation, output rounded to the
+// query dtype.  The reference's own kernel (benchmarks/paged_attention/native_paged_attention.hip)
+// runs one wave32 per (sequence, query head) serially over the context; this file is a different
+// design built for CDNA4:
+//
+//   pa_partition_kernel  one 256-thread workgroup per (sequence, KV head, head chunk, context
+//                        partition).  Each of its 4 waves walks 16-token tiles of the partition.
+//                        K rows are fetched as 16-byte lane loads straight into MFMA A operands
+//                        (tokens on M, query heads of the chunk replicated over N); V rows are
+//                        fetched as full-row lane-group loads (one token row per 16 lanes) and
+//                        consumed by fp32 FMAs.  The 16x16 MFMA accumulator layout puts the score
+//                        of token 4g+r for query head (j % GC) in lane 16g+j, register r -- the same
+//                        token that lane group g holds for V, so the only cross-lane traffic per
+//                        tile is a quad-DPP broadcast of probabilities between heads and a
+//                        permlane16/32 swap max-reduction.  Every KV byte is read once per
+//                        (KV head, head chunk) and shared by all query heads of the chunk.
+//   pa_reduce_kernel     deterministic fixed-order merge of the per-partition (max, sum, acc)
+//                        records.  Skipped for sequences that fit in one partition (the
+//                        partition kernel then writes the normalised output itself) and not
+//                        launched at all when one partition covers max_blocks * block_size.
+//
+// Scores are kept in the base-2 domain: x = (q . k) * scale * log2(e), p = exp2(x - m), which is
+// exp(q . k * scale - m') by the identity exp(y) = 2^(y * log2 e); v_exp_f32 evaluates 2^x.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "rk_paged_attention.h"
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWave * kWaves;
+constexpr int kTile = 16;             // tokens per wave step = MFMA M
+constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, plus one straddle
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------------------------
+// Element traits: 16-bit storage, fp32 math.
+struct Bf16 {
+  static __device__ __forceinline__ float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return __builtin_bit_cast(float, w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ uint16_t store(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+  }
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct Fp16 {
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+  }
+  static __device__ __forceinline__ uint16_t store(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  }
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// ---------------------------------------------------------------------------------------------
+// Cross-lane helpers (wave64).
+__device__ __forceinline__ uint32_t bits(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float fbits(uint32_t x) { return __builtin_bit_cast(float, x); }
+
+// DPP: quad_perm broadcast of quad lane H to all four lanes of each quad.
+template <int H>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return fbits(__builtin_amdgcn_update_dpp(0, bits(x), H * 0x55, 0xF, 0xF, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return fbits(__builtin_amdgcn_update_dpp(0, bits(x), CTRL, 0xF, 0xF, false));
+}
+
+// v_permlane16_swap exchanges odd 16-lane rows of its first operand with even rows of the second;
+// feeding the same value to both yields {x[l & ~16], x[l | 16]} per lane, so combining the pair
+// gives the xor-16 reduction in every lane.  v_permlane32_swap does the same for the two halves.
+__device__ __forceinline__ float max_xor16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(bits(x), bits(x), false, false);
+  return fmaxf(fbits(r[0]), fbits(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(bits(x), bits(x), false, false);
+  return fmaxf(fbits(r[0]), fbits(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(bits(x), bits(x), false, false);
+  return fbits(r[0]) + fbits(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(bits(x), bits(x), false, false);
+  return fbits(r[0]) + fbits(r[1]);
+}
+
+// Sum over the 16 lanes of each DPP row; every lane of the row receives the row total.
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  x += dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ int64_t load_index(const void* base, int64_t i, bool is64) {
+  return is64 ? static_cast<const int64_t*>(base)[i]
+              : static_cast<int64_t>(static_cast<const int32_t*>(base)[i]);
+}
+
+// ---------------------------------------------------------------------------------------------
+struct Params {
+  const uint16_t* __restrict__ q;
+  const uint16_t* __restrict__ k;
+  const uint16_t* __restrict__ v;
+  const void* __restrict__ block_tables;
+  const void* __restrict__ context_lengths;
+  uint16_t* __restrict__ out;
+  float* __restrict__ ws_acc;  // [batch, query_heads, num_partitions, D]
+  float* __restrict__ ws_ml;   // [batch, query_heads, num_partitions, 2] = (max, sum)
+  int64_t block_stride;        // elements between physical blocks: BS * Hkv * D
+  int64_t row_stride;          // elements between slots of a block: Hkv * D
+  int32_t batch;
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t group;        // query heads per KV head
+  int32_t head_chunks;  // ceil(group / GC)
+  int32_t num_blocks;
+  int32_t max_blocks;
+  int32_t bs_log2;
+  int32_t partition_tokens;
+  int32_t num_partitions;  // ceil(max_blocks * BS / partition_tokens)
+  int32_t index_is64;
+  float scale_log2e;
+};
+
+__device__ __forceinline__ int64_t clamped_context(const Params& p, int b) {
+  const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << p.bs_log2;
+  const int64_t ctx = load_index(p.context_lengths, b, p.index_is64 != 0);
+  return ctx < max_ctx ? ctx : max_ctx;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split-K partition kernel.
+//   E       element traits (Bf16 / Fp16)
+//   D       head_dim (64, 128, 256)
+//   GC      query heads handled per workgroup (1, 2, 4); all share one KV head
+//   QK_MFMA QK^T on MFMA (true) or on fp32 FMAs + DPP row sums (false)
+template <class E, int D, int GC, bool QK_MFMA>
+__global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
+  constexpr int KSTEPS = D / 32;  // MFMA k-steps (16-byte K chunks per lane per tile)
+  constexpr int VEC = D / 16;     // elements of a token row per lane (row = 16 lanes)
+  constexpr int VW = VEC / 2;     // 32-bit words per lane per token row
+  static_assert(GC == 1 || GC == 2 || GC == 4, "head chunk must be 1, 2 or 4");
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
+
+  __shared__ int s_table[kMaxSliceBlocks];
+  __shared__ float s_acc[kWaves][GC][D];
+  __shared__ float s_m[kWaves][GC];
+  __shared__ float s_l[kWaves][GC];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int g = lane >> 4;   // lane group: owns tokens 4g..4g+3 of every tile (V / scores)
+  const int j = lane & 15;   // lane in group: token j of the tile for K (MFMA), V column block
+
+  // Workgroup -> (sequence, KV head, head chunk, partition); partition index varies fastest.
+  const int64_t wg = blockIdx.x;
+  const int part = static_cast<int>(wg % p.num_partitions);
+  const int64_t rest = wg / p.num_partitions;
+  const int heads_per_seq = p.kv_heads * p.head_chunks;
+  const int hslot = static_cast<int>(rest % heads_per_seq);
+  const int b = static_cast<int>(rest / heads_per_seq);
+  const int kvh = hslot / p.head_chunks;
+  const int chunk = hslot % p.head_chunks;
+  const int head0 = kvh * p.group + chunk * GC;  // first query head of this chunk
+  const int heads_here = min(GC, p.group - chunk * GC);
+
+  const int64_t ctx = clamped_context(p, b);
+  if (ctx <= 0) {
+    // Softmax over an empty set: NaN, as the fallback produces.  Partition 0 owns the output.
+    if (part == 0) {
+      for (int idx = tid; idx < heads_here * D; idx += kThreads) {
+        const int h = idx / D, d = idx % D;
+        p.out[(static_cast<int64_t>(b) * p.query_heads + head0 + h) * D + d] =
+            E::store(__builtin_nanf(""));
+      }
+    }
+    return;
+  }
+  const int P = p.partition_tokens;
+  const int np = static_cast<int>((ctx + P - 1) / P);
+  if (part >= np) return;
+  const int p0 = part * P;
+  const int p_end = static_cast<int>(min(static_cast<int64_t>(p0 + P), ctx));
+  const int lb = p.bs_log2;
+  const int bs_mask = (1 << lb) - 1;
+
+  // Stage this partition's block-table slice in LDS (-1 marks ids outside [0, num_blocks)).
+  const int blk0 = p0 >> lb;
+  const int nblk = ((p_end - 1) >> lb) - blk0 + 1;
+  for (int i = tid; i < nblk; i += kThreads) {
+    const int64_t id = load_index(p.block_tables,
+                                  static_cast<int64_t>(b) * p.max_blocks + blk0 + i,
+                                  p.index_is64 != 0);
+    s_table[i] = (id >= 0 && id < p.num_blocks) ? static_cast<int>(id) : -1;
+  }
+
+  // Query operands.
+  const int64_t q_row0 = static_cast<int64_t>(b) * p.query_heads + head0;
+  const int my_head = j % GC;  // head of the scores this lane holds
+  u32x4 qB[QK_MFMA ? KSTEPS : 1];
+  float qf[QK_MFMA ? 1 : GC][QK_MFMA ? 1 : VEC];
+  if constexpr (QK_MFMA) {
+    // B operand of S^T = K Q^T: column n <-> query head (n % GC), k-chunk (4i + g) of 8 elements.
+    const bool ok = my_head < heads_here;
+    const uint16_t* src = p.q + (q_row0 + my_head) * D + g * 8;
+#pragma unroll
+    for (int i = 0; i < KSTEPS; ++i) {
+      qB[i] = ok ? *reinterpret_cast<const u32x4*>(src + i * 32) : u32x4{0, 0, 0, 0};
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+      const bool ok = h < heads_here;
+      const uint16_t* src = p.q + (q_row0 + h) * D + j * VEC;
+#pragma unroll
+      for (int w = 0; w < VW; ++w) {
+        const uint32_t word = ok ? reinterpret_cast<const uint32_t*>(src)[w] : 0u;
+        qf[h][2 * w] = E::lo(word);
+        qf[h][2 * w + 1] = E::hi(word);
+      }
+    }
+  }
+  __syncthreads();
+
+  const uint16_t* __restrict__ kbase = p.k + static_cast<int64_t>(kvh) * D;
+  const uint16_t* __restrict__ vbase = p.v + static_cast<int64_t>(kvh) * D;
+
+  struct Tile {
+    u32x4 k[QK_MFMA ? KSTEPS : 1];
+    uint32_t kr[QK_MFMA ? 1 : 4][QK_MFMA ? 1 : VW];
+    uint32_t v[4][VW];
+    uint32_t valid;  // bit r: token t0 + 4g + r is inside the partition and its block is valid
+  };
+
+  auto row_offset = [&](int t, int& pb) -> int64_t {
+    pb = (t < p_end) ? s_table[(t >> lb) - blk0] : -1;
+    return static_cast<int64_t>(pb) * p.block_stride + static_cast<int64_t>(t & bs_mask) * p.row_stride;
+  };
+
+  auto load_tile = [&](Tile& tile, int t0) {
+    if constexpr (QK_MFMA) {
+      int pb;
+      const int64_t off = row_offset(t0 + j, pb);
+      if (pb >= 0) {
+        const uint16_t* src = kbase + off + g * 8;
+#pragma unroll
+        for (int i = 0; i < KSTEPS; ++i) tile.k[i] = *reinterpret_cast<const u32x4*>(src + i * 32);
+      } else {
+#pragma unroll
+        for (int i = 0; i < KSTEPS; ++i) tile.k[i] = u32x4{0, 0, 0, 0};
+      }
+    }
+    tile.valid = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int pb;
+      const int64_t off = row_offset(t0 + 4 * g + r, pb) + j * VEC;
+      if (pb >= 0) {
+        tile.valid |= 1u << r;
+        const uint16_t* vsrc = vbase + off;
+        if constexpr (VW == 2) {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(vsrc);
+          tile.v[r][0] = x[0];
+          tile.v[r][1] = x[1];
+        } else {
+#pragma unroll
+          for (int w4 = 0; w4 < VW / 4; ++w4) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(vsrc + w4 * 8);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tile.v[r][w4 * 4 + e] = x[e];
+          }
+        }
+        if constexpr (!QK_MFMA) {
+          const uint16_t* ksrc = kbase + off;
+          if constexpr (VW == 2) {
+            const u32x2 x = *reinterpret_cast<const u32x2*>(ksrc);
+            tile.kr[r][0] = x[0];
+            tile.kr[r][1] = x[1];
+          } else {
+#pragma unroll
+            for (int w4 = 0; w4 < VW / 4; ++w4) {
+              const u32x4 x = *reinterpret_cast<const u32x4*>(ksrc + w4 * 8);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) tile.kr[r][w4 * 4 + e] = x[e];
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int w = 0; w < VW; ++w) tile.v[r][w] = 0u;
+        if constexpr (!QK_MFMA) {
+#pragma unroll
+          for (int w = 0; w < VW; ++w) tile.kr[r][w] = 0u;
+        }
+      }
+    }
+  };
+
+  // Online-softmax state.  m_own / l_own belong to head my_head (identical across lane groups
+  // after the per-tile reductions); acc covers every head of the chunk for this lane's columns.
+  const float neg_inf = -__builtin_inff();
+  float m_own = neg_inf;
+  float l_own = 0.0f;
+  float acc[GC][VEC];
+#pragma unroll
+  for (int h = 0; h < GC; ++h)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[h][e] = 0.0f;
+
+  auto compute_tile = [&](const Tile& tile) {
+    float x[4];
+    if constexpr (QK_MFMA) {
+      f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < KSTEPS; ++i) s = E::mfma(tile.k[i], qB[i], s);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = ((tile.valid >> r) & 1u) ? s[r] * p.scale_log2e : neg_inf;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float kf[VEC];
+#pragma unroll
+        for (int w = 0; w < VW; ++w) {
+          kf[2 * w] = E::lo(tile.kr[r][w]);
+          kf[2 * w + 1] = E::hi(tile.kr[r][w]);
+        }
+        float mine = 0.0f;
+#pragma unroll
+        for (int h = 0; h < GC; ++h) {
+          float dot = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) dot = fmaf(qf[h][e], kf[e], dot);
+          dot = row_sum16(dot);
+          mine = (h == my_head) ? dot : mine;
+        }
+        x[r] = ((tile.valid >> r) & 1u) ? mine * p.scale_log2e : neg_inf;
+      }
+    }
+
+    // Tile maximum for my_head over the 16 tokens (4 registers x 4 lane groups).
+    float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    tmax = max_xor16(tmax);
+    tmax = max_xor32(tmax);
+    const float m_new = fmaxf(m_own, tmax);
+    if (__builtin_amdgcn_ballot_w64(m_new > m_own) != 0) {
+      // Rescale all heads' accumulators: alpha_h = 2^(m_old_h - m_new_h), broadcast per quad.
+      const float alpha_own = fast_exp2(m_own - m_new);  // 0 when m_own = -inf
+      float alpha[GC];
+      if constexpr (GC == 1) {
+        alpha[0] = alpha_own;
+      } else {
+        alpha[0] = quad_bcast<0>(alpha_own);
+        alpha[1] = quad_bcast<1>(alpha_own);
+        if constexpr (GC == 4) {
+          alpha[2] = quad_bcast<2>(alpha_own);
+          alpha[3] = quad_bcast<3>(alpha_own);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < GC; ++h)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[h][e] *= alpha[h];
+      l_own *= alpha_own;
+      m_own = m_new;
+    }
+    const float m_use = (m_own == neg_inf) ? 0.0f : m_own;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(x[r] - m_use);
+    l_own += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+
+    // PV: token 4g + r, columns j*VEC .. j*VEC + VEC - 1, all heads of the chunk.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float ph[GC];
+      if constexpr (GC == 1) {
+        ph[0] = pr[r];
+      } else {
+        ph[0] = quad_bcast<0>(pr[r]);
+        ph[1] = quad_bcast<1>(pr[r]);
+        if constexpr (GC == 4) {
+          ph[2] = quad_bcast<2>(pr[r]);
+          ph[3] = quad_bcast<3>(pr[r]);
+        }
+      }
+#pragma unroll
+      for (int w = 0; w < VW; ++w) {
+        const float v0 = E::lo(tile.v[r][w]);
+        const float v1 = E::hi(tile.v[r][w]);
+#pragma unroll
+        for (int h = 0; h < GC; ++h) {
+          acc[h][2 * w] = fmaf(ph[h], v0, acc[h][2 * w]);
+          acc[h][2 * w + 1] = fmaf(ph[h], v1, acc[h][2 * w + 1]);
+        }
+      }
+    }
+  };
+
+  // Tiles of this wave: t0 = p0 + (wave + kWaves * n) * 16.  Register double buffering: the next
+  // tile's loads are in flight while the current tile is consumed.
+  const int step = kWaves * kTile;
+  int t0 = p0 + wave * kTile;
+  Tile ta, tb;
+  if (t0 < p_end) load_tile(ta, t0);
+  while (t0 < p_end) {
+    int t1 = t0 + step;
+    if (t1 < p_end) load_tile(tb, t1);
+    compute_tile(ta);
+    t0 = t1;
+    if (t0 >= p_end) break;
+    t1 = t0 + step;
+    if (t1 < p_end) load_tile(ta, t1);
+    compute_tile(tb);
+    t0 = t1;
+  }
+
+  // Wave totals: sum the four lane groups (they hold disjoint tokens, identical maxima).
+  l_own = sum_xor16(l_own);
+  l_own = sum_xor32(l_own);
+#pragma unroll
+  for (int h = 0; h < GC; ++h)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float a = sum_xor16(acc[h][e]);
+      acc[h][e] = sum_xor32(a);
+    }
+  if (g == 0) {
+#pragma unroll
+    for (int h = 0; h < GC; ++h)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s_acc[wave][h][j * VEC + e] = acc[h][e];
+    if (j < GC) {
+      s_m[wave][j] = m_own;
+      s_l[wave][j] = l_own;
+    }
+  }
+  __syncthreads();
+
+  // Merge the four waves (fixed order) and emit either the final output or a partition record.
+  const bool single = (np == 1);
+  for (int idx = tid; idx < heads_here * D; idx += kThreads) {
+    const int h = idx / D, d = idx % D;
+    float M = neg_inf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
+    float L = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = s_m[w][h];
+      const float f = (mw == neg_inf) ? 0.0f : fast_exp2(mw - M);
+      L = fmaf(s_l[w][h], f, L);
+      A = fmaf(s_acc[w][h][d], f, A);
+    }
+    const int64_t row = q_row0 + h;
+    if (single) {
+      p.out[row * D + d] = E::store(A / L);
+    } else {
+      const int64_t rec = row * p.num_partitions + part;
+      p.ws_acc[rec * D + d] = A;
+      if (d == 0) {
+        p.ws_ml[rec * 2] = M;
+        p.ws_ml[rec * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Partition reduce: one wave per (sequence, query head); partitions merged in index order.
+template <class E, int D>
+__global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
+  constexpr int PER_LANE = D / kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= static_cast<int64_t>(p.batch) * p.query_heads) return;
+  const int b = static_cast<int>(row / p.query_heads);
+  const int64_t ctx = clamped_context(p, b);
+  if (ctx <= 0) return;  // written by the partition kernel
+  const int np = static_cast<int>((ctx + p.partition_tokens - 1) / p.partition_tokens);
+  if (np <= 1) return;   // written by the partition kernel
+  const float* ml = p.ws_ml + row * p.num_partitions * 2;
+  const float* acc = p.ws_acc + row * p.num_partitions * D;
+  const float neg_inf = -__builtin_inff();
+  float M = neg_inf;
+  for (int i = 0; i < np; ++i) M = fmaxf(M, ml[2 * i]);
+  float L = 0.0f;
+  float A[PER_LANE];
+#pragma unroll
+  for (int c = 0; c < PER_LANE; ++c) A[c] = 0.0f;
+  for (int i = 0; i < np; ++i) {
+    const float mi = ml[2 * i];
+    const float f = (mi == neg_inf) ? 0.0f : fast_exp2(mi - M);
+    L = fmaf(ml[2 * i + 1], f, L);
+#pragma unroll
+    for (int c = 0; c < PER_LANE; ++c) A[c] = fmaf(acc[static_cast<int64_t>(i) * D + lane + c * kWave], f, A[c]);
+  }
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int c = 0; c < PER_LANE; ++c) p.out[row * D + lane + c * kWave] = E::store(A[c] * inv);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side.
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buffer[512];
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(buffer, sizeof(buffer), fmt, args);
+  va_end(args);
+  g_last_error = buffer;
+  return code;
+}
+
+int head_chunk_for(int64_t group) {
+  if (group == 1) return 1;
+  if (group == 2) return 2;
+  return 4;
+}
+
+int log2_exact(int64_t x) {
+  int r = 0;
+  while ((int64_t{1} << r) < x) ++r;
+  return ((int64_t{1} << r) == x) ? r : -1;
+}
+
+struct Shape {
+  int64_t batch, query_heads, kv_heads, head_dim, num_blocks, block_size, max_blocks, partition;
+  int64_t num_partitions;
+};
+
+int check_shape(const Shape& s) {
+  if (s.batch <= 0 || s.query_heads <= 0 || s.kv_heads <= 0 || s.num_blocks <= 0 ||
+      s.block_size <= 0 || s.max_blocks <= 0)
+    return fail(RK_ERR_INVALID_ARGUMENT, "tensor dimensions must be positive");
+  if (s.head_dim != 64 && s.head_dim != 128 && s.head_dim != 256)
+    return fail(RK_ERR_INVALID_ARGUMENT, "head_dim must be one of 64, 128, 256 (got %lld)",
+                static_cast<long long>(s.head_dim));
+  if (s.query_heads % s.kv_heads != 0)
+    return fail(RK_ERR_INVALID_ARGUMENT, "query_heads must be divisible by kv_heads");
+  if (log2_exact(s.block_size) < 0 || s.block_size > 256)
+    return fail(RK_ERR_UNSUPPORTED, "block_size must be a power of two <= 256 (got %lld)",
+                static_cast<long long>(s.block_size));
+  if (s.partition < kTile || s.partition > 8192 || s.partition % kTile != 0)
+    return fail(RK_ERR_INVALID_ARGUMENT,
+                "partition_tokens must be a multiple of 16 in [16, 8192] (got %lld)",
+                static_cast<long long>(s.partition));
+  if (s.partition / s.block_size > kMaxSliceBlocks - 1)
+    return fail(RK_ERR_INVALID_ARGUMENT, "partition_tokens / block_size must be <= 256");
+  if (s.num_blocks >= (int64_t{1} << 31) || s.max_blocks * s.block_size >= (int64_t{1} << 31) ||
+      s.batch >= (int64_t{1} << 31) || s.query_heads >= (int64_t{1} << 20))
+    return fail(RK_ERR_UNSUPPORTED, "shape exceeds the 32-bit index range of this kernel");
+  return RK_OK;
+}
+
+int64_t partitions_for(const Shape& s) {
+  return (s.max_blocks * s.block_size + s.partition - 1) / s.partition;
+}
+
+size_t workspace_for(const Shape& s) {
+  if (s.num_partitions <= 1) return 0;
+  const size_t records = static_cast<size_t>(s.batch) * s.query_heads * s.num_partitions;
+  const size_t acc = records * s.head_dim * sizeof(float);
+  const size_t acc_padded = (acc + 255) & ~size_t{255};
+  return acc_padded + records * 2 * sizeof(float);
+}
+
+template <class E, int D, int GC>
+hipError_t launch_partition(const Params& prm, int variant, int64_t grid, hipStream_t stream) {
+  if (variant == RK_PA_VARIANT_MFMA) {
+    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, true>), dim3(static_cast<uint32_t>(grid)),
+                       dim3(kThreads), 0, stream, prm);
+  } else {
+    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, false>), dim3(static_cast<uint32_t>(grid)),
+                       dim3(kThreads), 0, stream, prm);
+  }
+  return hipGetLastError();
+}
+
+template <class E, int D>
+hipError_t launch_all(const Params& prm, int gc, int variant, int64_t grid, bool reduce,
+                      hipStream_t stream) {
+  hipError_t err;
+  if (gc == 1)
+    err = launch_partition<E, D, 1>(prm, variant, grid, stream);
+  else if (gc == 2)
+    err = launch_partition<E, D, 2>(prm, variant, grid, stream);
+  else
+    err = launch_partition<E, D, 4>(prm, variant, grid, stream);
+  if (err != hipSuccess || !reduce) return err;
+  const int64_t rows = static_cast<int64_t>(prm.batch) * prm.query_heads;
+  const int64_t rgrid = (rows + kWaves - 1) / kWaves;
+  hipLaunchKernelGGL((pa_reduce_kernel<E, D>), dim3(static_cast<uint32_t>(rgrid)), dim3(kThreads),
+                     0, stream, prm);
+  return hipGetLastError();
+}
+
+template <class E>
+hipError_t launch_dtype(const Params& prm, int64_t head_dim, int gc, int variant, int64_t grid,
+                        bool reduce, hipStream_t stream) {
+  if (head_dim == 64) return launch_all<E, 64>(prm, gc, variant, grid, reduce, stream);
+  if (head_dim == 128) return launch_all<E, 128>(prm, gc, variant, grid, reduce, stream);
+  return launch_all<E, 256>(prm, gc, variant, grid, reduce, stream);
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t head_dim,
+                                            int64_t block_size, int64_t max_blocks_per_sequence,
+                                            int64_t partition_tokens, size_t* bytes) {
+  if (bytes == nullptr) return fail(RK_ERR_INVALID_ARGUMENT, "bytes must not be NULL");
+  Shape s{batch, query_heads, 1, head_dim, 1, block_size, max_blocks_per_sequence, partition_tokens, 0};
+  const int status = check_shape(s);
+  if (status != RK_OK) return status;
+  s.num_partitions = partitions_for(s);
+  *bytes = workspace_for(s);
+  return RK_OK;
+}
+
+extern "C" int rk_pa_decode(const void* query, const void* key_cache, const void* value_cache,
+                            const void* block_tables, const void* context_lengths, void* output,
+                            void* workspace, size_t workspace_bytes, int64_t batch,
+                            int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                            int64_t num_blocks, int64_t block_size,
+                            int64_t max_blocks_per_sequence, float scale, int dtype,
+                            int index_dtype, int64_t partition_tokens, int variant, void* stream) {
+  if (!query || !key_cache || !value_cache || !block_tables || !context_lengths || !output)
+    return fail(RK_ERR_INVALID_ARGUMENT, "tensor pointers must not be NULL");
+  if (dtype != RK_DTYPE_FP16 && dtype != RK_DTYPE_BF16)
+    return fail(RK_ERR_INVALID_ARGUMENT, "dtype must be RK_DTYPE_FP16 or RK_DTYPE_BF16");
+  if (index_dtype != RK_INDEX_INT32 && index_dtype != RK_INDEX_INT64)
+    return fail(RK_ERR_INVALID_ARGUMENT, "index_dtype must be RK_INDEX_INT32 or RK_INDEX_INT64");
+  if (variant != RK_PA_VARIANT_MFMA && variant != RK_PA_VARIANT_VALU)
+    return fail(RK_ERR_INVALID_ARGUMENT, "unknown kernel variant %d", variant);
+  if (!(scale > 0.0f) || !isfinite(scale))
+    return fail(RK_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
+  if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(output))
+    return fail(RK_ERR_UNSUPPORTED, "query, caches and output must be 16-byte aligned");
+
+  Shape s{batch, query_heads, kv_heads, head_dim, num_blocks, block_size, max_blocks_per_sequence,
+          partition_tokens, 0};
+  int status = check_shape(s);
+  if (status != RK_OK) return status;
+  s.num_partitions = partitions_for(s);
+  const size_t need = workspace_for(s);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(RK_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(RK_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+
+  const int64_t group = query_heads / kv_heads;
+  const int gc = head_chunk_for(group);
+  const int64_t head_chunks = (group + gc - 1) / gc;
+  const int64_t grid = batch * kv_heads * head_chunks * s.num_partitions;
+  if (grid >= (int64_t{1} << 31))
+    return fail(RK_ERR_UNSUPPORTED, "launch grid exceeds 2^31 workgroups");
+
+  Params prm{};
+  prm.q = static_cast<const uint16_t*>(query);
+  prm.k = static_cast<const uint16_t*>(key_cache);
+  prm.v = static_cast<const uint16_t*>(value_cache);
+  prm.block_tables = block_tables;
+  prm.context_lengths = context_lengths;
+  prm.out = static_cast<uint16_t*>(output);
+  if (need > 0) {
+    const size_t records = static_cast<size_t>(batch) * query_heads * s.num_partitions;
+    const size_t acc_bytes = (records * head_dim * sizeof(float) + 255) & ~size_t{255};
+    prm.ws_acc = static_cast<float*>(workspace);
+    prm.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
+  }
+  prm.block_stride = block_size * kv_heads * head_dim;
+  prm.row_stride = kv_heads * head_dim;
+  prm.batch = static_cast<int32_t>(batch);
+  prm.query_heads = static_cast<int32_t>(query_heads);
+  prm.kv_heads = static_cast<int32_t>(kv_heads);
+  prm.group = static_cast<int32_t>(group);
+  prm.head_chunks = static_cast<int32_t>(head_chunks);
+  prm.num_blocks = static_cast<int32_t>(num_blocks);
+  prm.max_blocks = static_cast<int32_t>(max_blocks_per_sequence);
+  prm.bs_log2 = log2_exact(block_size);
+  prm.partition_tokens = static_cast<int32_t>(partition_tokens);
+  prm.num_partitions = static_cast<int32_t>(s.num_partitions);
+  prm.index_is64 = index_dtype == RK_INDEX_INT64 ? 1 : 0;
+  prm.scale_log2e = scale * kLog2e;
+
+  const bool reduce = s.num_partitions > 1;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const hipError_t err =
+      dtype == RK_DTYPE_BF16
+          ? launch_dtype<Bf16>(prm, head_dim, gc, variant, grid, reduce, hs)
+          : launch_dtype<Fp16>(prm, head_dim, gc, variant, grid, reduce, hs);
+  if (err != hipSuccess)
+    return fail(RK_ERR_LAUNCH, "paged attention launch failed: %s", hipGetErrorString(err));
+  return RK_OK;
+}
+
+extern "C" const char* rk_pa_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" const char* rk_pa_version(void) { return "rk_pa_gfx950 1.0.0 (gfx950, wave64)"; }

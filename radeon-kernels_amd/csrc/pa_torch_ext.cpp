@@ -1,0 +1,133 @@
+// PyTorch-ROCm binding of the gfx950 paged-attention decode library (include/rk_paged_attention.h).
+//
+// This is the python_extension artifact that dispatch entries name.  Its entrypoints keep the
+// calling convention of the reference bindings (benchmarks/paged_attention/native_paged_attention.hip:244-283,
+// invoked by src/radeon_kernels/providers/native.py:25 as entrypoint(q, k, v, bt, cl, scale, **launch)):
+// they validate, allocate the output (and the split-K workspace) from the caching allocator on the
+// current HIP stream, launch asynchronously and return the new tensor.  No host synchronisation,
+// no device-to-host reads: safe under HIP graph capture.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPStream.h>
+
+#include <cmath>
+#include <string>
+
+#include "rk_paged_attention.h"
+
+namespace {
+
+void check_data(const at::Tensor& t, const char* name, int64_t rank) {
+  TORCH_CHECK_VALUE(t.is_cuda(), name, " must be a ROCm tensor");
+  TORCH_CHECK_VALUE(t.dim() == rank, name, " must be rank ", rank);
+  TORCH_CHECK_VALUE(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK_TYPE(t.scalar_type() == at::kHalf || t.scalar_type() == at::kBFloat16, name,
+                   " must use FP16 or BF16");
+}
+
+void check_index(const at::Tensor& t, const char* name, int64_t rank) {
+  TORCH_CHECK_VALUE(t.is_cuda(), name, " must be a ROCm tensor");
+  TORCH_CHECK_VALUE(t.dim() == rank, name, " must be rank ", rank);
+  TORCH_CHECK_VALUE(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK_TYPE(t.scalar_type() == at::kInt || t.scalar_type() == at::kLong, name,
+                   " must use INT32 or INT64");
+}
+
+void raise_status(int status) {
+  const std::string message = rk_pa_last_error();
+  if (status == RK_ERR_INVALID_ARGUMENT || status == RK_ERR_UNSUPPORTED) {
+    TORCH_CHECK_VALUE(false, "rk_pa_gfx950: ", message);
+  }
+  TORCH_CHECK(false, "rk_pa_gfx950: ", message);
+}
+
+at::Tensor decode(const at::Tensor& query, const at::Tensor& key_cache,
+                  const at::Tensor& value_cache, const at::Tensor& block_tables,
+                  const at::Tensor& context_lengths, double scale, int64_t partition_tokens,
+                  int variant) {
+  check_data(query, "query", 3);
+  check_data(key_cache, "key_cache", 4);
+  check_data(value_cache, "value_cache", 4);
+  check_index(block_tables, "block_tables", 2);
+  check_index(context_lengths, "context_lengths", 1);
+  const auto device = query.device();
+  TORCH_CHECK_VALUE(key_cache.device() == device && value_cache.device() == device &&
+                        block_tables.device() == device && context_lengths.device() == device,
+                    "all tensors must be on the query device");
+  TORCH_CHECK_TYPE(key_cache.scalar_type() == query.scalar_type() &&
+                       value_cache.scalar_type() == query.scalar_type(),
+                   "query and cache dtypes must match");
+  TORCH_CHECK_TYPE(block_tables.scalar_type() == context_lengths.scalar_type(),
+                   "index dtypes must match");
+  TORCH_CHECK_VALUE(key_cache.sizes() == value_cache.sizes(), "K/V cache shapes must match");
+  TORCH_CHECK_VALUE(block_tables.size(0) == query.size(0), "block table batch must match query");
+  TORCH_CHECK_VALUE(context_lengths.size(0) == query.size(0),
+                    "context length batch must match query");
+  TORCH_CHECK_VALUE(query.size(2) == key_cache.size(3),
+                    "query and cache head dimensions must match");
+  TORCH_CHECK_VALUE(std::isfinite(scale) && scale > 0.0, "scale must be positive and finite");
+  TORCH_CHECK_VALUE(!query.requires_grad() && !key_cache.requires_grad() &&
+                        !value_cache.requires_grad(),
+                    "paged attention decode is inference-only");
+
+  const int64_t batch = query.size(0);
+  const int64_t query_heads = query.size(1);
+  const int64_t head_dim = query.size(2);
+  const int64_t num_blocks = key_cache.size(0);
+  const int64_t block_size = key_cache.size(1);
+  const int64_t kv_heads = key_cache.size(2);
+  const int64_t max_blocks = block_tables.size(1);
+  const int dtype = query.scalar_type() == at::kBFloat16 ? RK_DTYPE_BF16 : RK_DTYPE_FP16;
+  const int index_dtype = block_tables.scalar_type() == at::kLong ? RK_INDEX_INT64 : RK_INDEX_INT32;
+
+  size_t workspace_bytes = 0;
+  int status = rk_pa_decode_workspace_bytes(batch, query_heads, head_dim, block_size, max_blocks,
+                                            partition_tokens, &workspace_bytes);
+  if (status != RK_OK) raise_status(status);
+
+  at::DeviceGuard guard(device);
+  at::Tensor output = at::empty_like(query);
+  at::Tensor workspace;
+  void* workspace_ptr = nullptr;
+  if (workspace_bytes > 0) {
+    workspace = at::empty({static_cast<int64_t>(workspace_bytes)}, query.options().dtype(at::kByte));
+    workspace_ptr = workspace.data_ptr();
+  }
+  hipStream_t stream = c10::hip::getCurrentHIPStream(device.index()).stream();
+  status = rk_pa_decode(query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                        block_tables.data_ptr(), context_lengths.data_ptr(), output.data_ptr(),
+                        workspace_ptr, workspace_bytes, batch, query_heads, kv_heads, head_dim,
+                        num_blocks, block_size, max_blocks, static_cast<float>(scale), dtype,
+                        index_dtype, partition_tokens, variant, stream);
+  if (status != RK_OK) raise_status(status);
+  return output;
+}
+
+at::Tensor decode_mfma(const at::Tensor& query, const at::Tensor& key_cache,
+                       const at::Tensor& value_cache, const at::Tensor& block_tables,
+                       const at::Tensor& context_lengths, double scale, int64_t partition_tokens) {
+  return decode(query, key_cache, value_cache, block_tables, context_lengths, scale,
+                partition_tokens, RK_PA_VARIANT_MFMA);
+}
+
+at::Tensor decode_valu(const at::Tensor& query, const at::Tensor& key_cache,
+                       const at::Tensor& value_cache, const at::Tensor& block_tables,
+                       const at::Tensor& context_lengths, double scale, int64_t partition_tokens) {
+  return decode(query, key_cache, value_cache, block_tables, context_lengths, scale,
+                partition_tokens, RK_PA_VARIANT_VALU);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(rk_pa_gfx950, module) {
+  module.doc() = "gfx950 split-K paged-attention decode (MFMA QK^T or VALU QK^T, VALU PV)";
+  module.def("decode_mfma", &decode_mfma, "paged decode, QK^T on MFMA", py::arg("query"),
+             py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
+             py::arg("context_lengths"), py::arg("scale"), py::kw_only(),
+             py::arg("partition_tokens") = 512);
+  module.def("decode_valu", &decode_valu, "paged decode, QK^T on fp32 FMAs", py::arg("query"),
+             py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
+             py::arg("context_lengths"), py::arg("scale"), py::kw_only(),
+             py::arg("partition_tokens") = 512);
+  module.def("version", []() { return std::string(rk_pa_version()); });
+}

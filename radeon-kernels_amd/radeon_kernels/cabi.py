@@ -1,0 +1,129 @@
+"""ctypes binding of the C ABI in ``include/rk_paged_attention.h`` (``librk_pa_gfx950.so``).
+
+This is the boundary a non-Python host (or a test) uses: plain device pointers, int64 sizes and a
+HIP stream handle.  ``decode`` adapts torch tensors to it (allocating the output and split-K
+workspace with torch on the current stream).  Loading fails loudly if the library was not built;
+there is no fallback here.
+
+torch is imported before the library is opened so that the library binds to the HIP runtime torch
+already loaded (both carry the soname ``libamdhip64.so.7``) instead of loading a second copy.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+from typing import Any
+
+LIBRARY_PATH = Path(__file__).resolve().parents[1] / "packs" / "gfx950" / "lib" / "librk_pa_gfx950.so"
+
+RK_OK = 0
+RK_ERR_INVALID_ARGUMENT = 1
+RK_ERR_UNSUPPORTED = 2
+RK_ERR_WORKSPACE = 3
+RK_ERR_LAUNCH = 4
+RK_DTYPE_FP16 = 0
+RK_DTYPE_BF16 = 1
+RK_INDEX_INT32 = 0
+RK_INDEX_INT64 = 1
+VARIANTS = {"mfma": 0, "valu": 1}
+
+EXPORTED_SYMBOLS = ("rk_pa_decode", "rk_pa_decode_workspace_bytes", "rk_pa_last_error", "rk_pa_version")
+
+
+class CabiError(RuntimeError):
+    def __init__(self, status: int, message: str) -> None:
+        self.status = status
+        super().__init__(f"rk_pa status {status}: {message}")
+
+
+class PagedAttentionLibrary:
+    def __init__(self, path: Path | str | None = None) -> None:
+        import torch  # noqa: F401  (bind to torch's HIP runtime, see module docstring)
+
+        self.path = Path(path) if path is not None else LIBRARY_PATH
+        if not self.path.is_file():
+            raise FileNotFoundError(
+                f"native library {self.path} is missing; build it with `python radeon-kernels_amd/build.py`"
+            )
+        lib = ctypes.CDLL(str(self.path))
+        i64, vp, sz = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+        lib.rk_pa_decode_workspace_bytes.argtypes = [i64, i64, i64, i64, i64, i64, ctypes.POINTER(sz)]
+        lib.rk_pa_decode_workspace_bytes.restype = ctypes.c_int
+        lib.rk_pa_decode.argtypes = [vp, vp, vp, vp, vp, vp, vp, sz, i64, i64, i64, i64, i64, i64, i64,
+                                     ctypes.c_float, ctypes.c_int, ctypes.c_int, i64, ctypes.c_int, vp]
+        lib.rk_pa_decode.restype = ctypes.c_int
+        lib.rk_pa_last_error.argtypes = []
+        lib.rk_pa_last_error.restype = ctypes.c_char_p
+        lib.rk_pa_version.argtypes = []
+        lib.rk_pa_version.restype = ctypes.c_char_p
+        self.lib = lib
+
+    def version(self) -> str:
+        return self.lib.rk_pa_version().decode()
+
+    def last_error(self) -> str:
+        return self.lib.rk_pa_last_error().decode()
+
+    def check(self, status: int) -> None:
+        if status != RK_OK:
+            raise CabiError(status, self.last_error())
+
+    def workspace_bytes(self, batch: int, query_heads: int, head_dim: int, block_size: int, max_blocks: int,
+                        partition_tokens: int) -> int:
+        out = ctypes.c_size_t(0)
+        self.check(self.lib.rk_pa_decode_workspace_bytes(batch, query_heads, head_dim, block_size, max_blocks,
+                                                         partition_tokens, ctypes.byref(out)))
+        return int(out.value)
+
+    def decode_raw(self, *, query: int, key_cache: int, value_cache: int, block_tables: int, context_lengths: int,
+                   output: int, workspace: int, workspace_bytes: int, batch: int, query_heads: int, kv_heads: int,
+                   head_dim: int, num_blocks: int, block_size: int, max_blocks: int, scale: float, dtype: int,
+                   index_dtype: int, partition_tokens: int, variant: int, stream: int) -> int:
+        return self.lib.rk_pa_decode(query, key_cache, value_cache, block_tables, context_lengths, output,
+                                     workspace or None, workspace_bytes, batch, query_heads, kv_heads, head_dim,
+                                     num_blocks, block_size, max_blocks, ctypes.c_float(scale), dtype, index_dtype,
+                                     partition_tokens, variant, stream or None)
+
+    def decode(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
+               scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
+               out: Any | None = None, workspace: Any | None = None, stream: Any | None = None) -> Any:
+        """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None)."""
+
+        import torch
+
+        batch, query_heads, head_dim = (int(s) for s in query.shape)
+        num_blocks, block_size, kv_heads, _ = (int(s) for s in key_cache.shape)
+        max_blocks = int(block_tables.shape[1])
+        if scale is None:
+            scale = 1.0 / math.sqrt(head_dim)
+        need = self.workspace_bytes(batch, query_heads, head_dim, block_size, max_blocks, partition_tokens)
+        if out is None:
+            out = torch.empty_like(query)
+        if need and workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
+        if stream is None:
+            stream = torch.cuda.current_stream(query.device)
+        status = self.decode_raw(
+            query=query.data_ptr(), key_cache=key_cache.data_ptr(), value_cache=value_cache.data_ptr(),
+            block_tables=block_tables.data_ptr(), context_lengths=context_lengths.data_ptr(), output=out.data_ptr(),
+            workspace=workspace.data_ptr() if need else 0, workspace_bytes=workspace.numel() if need else 0,
+            batch=batch, query_heads=query_heads, kv_heads=kv_heads, head_dim=head_dim, num_blocks=num_blocks,
+            block_size=block_size, max_blocks=max_blocks, scale=float(scale),
+            dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
+            index_dtype=RK_INDEX_INT64 if block_tables.dtype == torch.int64 else RK_INDEX_INT32,
+            partition_tokens=partition_tokens, variant=VARIANTS[variant], stream=stream.cuda_stream,
+        )
+        self.check(status)
+        return out
+
+
+_LIBRARY: PagedAttentionLibrary | None = None
+
+
+def library() -> PagedAttentionLibrary:
+    global _LIBRARY
+    if _LIBRARY is None:
+        _LIBRARY = PagedAttentionLibrary()
+    return _LIBRARY

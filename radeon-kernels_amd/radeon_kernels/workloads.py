@@ -1,0 +1,160 @@
+"""Seeded paged-decode workloads: the five measured shapes and a generic builder.
+
+Each workload fixes batch, heads, head_dim, block size, dtype, cache size and how block tables and
+context lengths are drawn.  Inputs come from a ``torch.Generator`` seeded per workload, drawn in a
+fixed order (context lengths, block permutation, query, keys, values) so that a seed names one
+input set.  Generation on the CPU is bit-reproducible on every machine; generation on a GPU is
+reproducible for a given torch build and is used for the 4.5 GB ragged workload.
+
+KV accounting (``kv_bytes``) counts the K and V rows a decode must read: for every sequence,
+``min(context, max_blocks * block_size)`` tokens x kv_heads x head_dim x 2 tensors x element size.
+Padding table entries and tokens past the context are not counted.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Any
+
+DEFAULT_SEED_BASE = 20261201
+
+
+@dataclass(frozen=True)
+class Workload:
+    key: str
+    name: str
+    batch: int
+    query_heads: int
+    kv_heads: int
+    head_dim: int
+    block_size: int
+    dtype: str  # "fp16" | "bf16"
+    max_blocks: int
+    num_blocks: int | None  # None: sum of blocks the drawn contexts need (ragged workload)
+    context: int | tuple[int, int]  # fixed length, or inclusive uniform range
+    kv_std: float = 1.0
+    seed: int = DEFAULT_SEED_BASE
+    notes: str = ""
+    extra: dict[str, Any] = field(default_factory=dict)
+
+    @property
+    def ragged(self) -> bool:
+        return isinstance(self.context, tuple)
+
+    @property
+    def elem_size(self) -> int:
+        return 2
+
+
+WORKLOADS: dict[str, Workload] = {
+    "c1": Workload(
+        key="c1", name="b1-gqa32x8-c128-d128-p16-fp16", batch=1, query_heads=32, kv_heads=8, head_dim=128,
+        block_size=16, dtype="fp16", max_blocks=8, num_blocks=64, context=128, seed=DEFAULT_SEED_BASE + 0,
+        notes="block table = first 8 entries of a seeded permutation of 0..63",
+    ),
+    "c2": Workload(
+        key="c2", name="b8-gqa32x8-c1024-d128-p16-bf16", batch=8, query_heads=32, kv_heads=8, head_dim=128,
+        block_size=16, dtype="bf16", max_blocks=64, num_blocks=1024, context=1024, seed=DEFAULT_SEED_BASE + 1,
+        notes="64 block ids per sequence drawn without replacement from a seeded permutation of 0..1023",
+    ),
+    "c3": Workload(
+        key="c3", name="b4-mha16-c2048-d64-p32-bf16", batch=4, query_heads=16, kv_heads=16, head_dim=64,
+        block_size=32, dtype="bf16", max_blocks=64, num_blocks=512, context=2048, seed=DEFAULT_SEED_BASE + 2,
+        notes="disjoint seeded block tables of 64 blocks each",
+    ),
+    "c4": Workload(
+        key="c4", name="b4-gqa32x8-c1024-d256-p16-fp16", batch=4, query_heads=32, kv_heads=8, head_dim=256,
+        block_size=16, dtype="fp16", max_blocks=64, num_blocks=512, context=1024, kv_std=0.5,
+        seed=DEFAULT_SEED_BASE + 3, notes="K/V ~ N(0, 0.5^2) (0.5 read as the standard deviation)",
+    ),
+    "c5": Workload(
+        key="c5", name="b128-gqa32x8-ragged1024to16384-d128-p16-bf16", batch=128, query_heads=32, kv_heads=8,
+        head_dim=128, block_size=16, dtype="bf16", max_blocks=1024, num_blocks=None, context=(1024, 16384),
+        seed=DEFAULT_SEED_BASE + 4,
+        notes="context ~ U[1024, 16384]; tables padded to 1024 with block 0; blocks assigned by seeded shuffle",
+    ),
+}
+
+
+def torch_dtype(torch: Any, name: str) -> Any:
+    return {"fp16": torch.float16, "bf16": torch.bfloat16}[name]
+
+
+def make_inputs(
+    workload: Workload | str,
+    *,
+    seed: int | None = None,
+    device: Any = "cpu",
+    generator_device: Any | None = None,
+    index_dtype: str = "int32",
+    torch_module: Any | None = None,
+) -> dict[str, Any]:
+    """Draw the workload's tensors; returns query, key_cache, value_cache, block_tables,
+    context_lengths (all on ``device``) plus ``num_blocks`` and ``kv_bytes``."""
+
+    if torch_module is None:
+        import torch as torch_module
+    torch = torch_module
+    w = WORKLOADS[workload] if isinstance(workload, str) else workload
+    seed = w.seed if seed is None else seed
+    gen_device = torch.device(generator_device if generator_device is not None else "cpu")
+    generator = torch.Generator(device=gen_device).manual_seed(seed)
+    index = {"int32": torch.int32, "int64": torch.int64}[index_dtype]
+    dtype = torch_dtype(torch, w.dtype)
+
+    if w.ragged:
+        low, high = w.context
+        contexts = torch.randint(low, high + 1, (w.batch,), generator=generator, device=gen_device).cpu()
+    else:
+        contexts = torch.full((w.batch,), int(w.context), dtype=torch.int64)
+    needed = [math.ceil(int(c) / w.block_size) for c in contexts]
+    if w.num_blocks is None:
+        num_blocks = int(sum(needed))
+        permutation = torch.randperm(num_blocks, generator=generator, device=gen_device).cpu()
+        tables = torch.zeros((w.batch, w.max_blocks), dtype=torch.int64)
+        cursor = 0
+        for b, count in enumerate(needed):
+            tables[b, :count] = permutation[cursor : cursor + count]
+            cursor += count
+    else:
+        num_blocks = w.num_blocks
+        permutation = torch.randperm(num_blocks, generator=generator, device=gen_device).cpu()
+        tables = permutation[: w.batch * w.max_blocks].view(w.batch, w.max_blocks).clone()
+
+    def normal(shape: tuple[int, ...], std: float) -> Any:
+        values = torch.randn(shape, generator=generator, device=gen_device, dtype=torch.float32)
+        if std != 1.0:
+            values.mul_(std)
+        return values.to(dtype=dtype)
+
+    cache_shape = (num_blocks, w.block_size, w.kv_heads, w.head_dim)
+    query = normal((w.batch, w.query_heads, w.head_dim), 1.0)
+    key_cache = normal(cache_shape, w.kv_std)
+    value_cache = normal(cache_shape, w.kv_std)
+    return {
+        "query": query.to(device),
+        "key_cache": key_cache.to(device),
+        "value_cache": value_cache.to(device),
+        "block_tables": tables.to(dtype=index).to(device),
+        "context_lengths": contexts.to(dtype=index).to(device),
+        "num_blocks": num_blocks,
+        "kv_bytes": kv_bytes(w, [int(c) for c in contexts]),
+        "workload": w,
+        "seed": seed,
+    }
+
+
+def kv_bytes(workload: Workload, contexts: list[int]) -> int:
+    cap = workload.max_blocks * workload.block_size
+    tokens = sum(min(max(int(c), 0), cap) for c in contexts)
+    return tokens * workload.kv_heads * workload.head_dim * 2 * workload.elem_size
+
+
+def aux_bytes(workload: Workload, contexts: list[int], index_size: int = 4) -> int:
+    """Query + output + block-table entries + context lengths a decode touches."""
+
+    qo = 2 * workload.batch * workload.query_heads * workload.head_dim * workload.elem_size
+    cap = workload.max_blocks * workload.block_size
+    table = sum(math.ceil(min(max(int(c), 0), cap) / workload.block_size) for c in contexts) * index_size
+    return qo + table + workload.batch * index_size

@@ -1,0 +1,40 @@
+"""Test configuration: import paths, the ``gpu`` marker and shared fixtures."""
+
+from __future__ import annotations
+
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+PACKAGE_DIR = ROOT / "radeon-kernels_amd"
+for entry in (str(ROOT), str(PACKAGE_DIR)):
+    if entry not in sys.path:
+        sys.path.insert(0, entry)
+
+
+def pytest_configure(config: pytest.Config) -> None:
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; run with -m gpu on the GPU host")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The first visible gfx950 device, or skip."""
+
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no visible ROCm GPU")
+    arch = torch.cuda.get_device_properties(0).gcnArchName.split(":", 1)[0]
+    if arch != "gfx950":
+        pytest.skip(f"needs gfx950, found {arch}")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def palib(gpu):
+    from radeon_kernels.cabi import library
+
+    return library()

@@ -1,0 +1,134 @@
+"""GPU acceptance through the public API: ``rk.paged_attention_decode`` must select the gfx950 winner.
+
+Mirrors the reference's release acceptance (developer/promotion/verify_paged_attention_release.py:
+26-150): compilation is never triggered, the explain record names the exact entry and
+``native/<entrypoint>``, uncovered shapes run the declared torch fallback with an exact match, and
+(contracts/paged_attention_decode-1.0.json:23) the call is graph-capturable and deterministic.
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from _helpers import announce, assert_within, make_case, oracle64, to_device
+
+pytestmark = pytest.mark.gpu
+
+ENTRY_IDS = {
+    "c1": "paged_attention_decode-gfx950-b1-gqa32x8-c128-d128-p16-fp16",
+    "c2": "paged_attention_decode-gfx950-b8-gqa32x8-c1024-d128-p16-bf16",
+    "c3": "paged_attention_decode-gfx950-b4-mha16-c2048-d64-p32-bf16",
+    "c4": "paged_attention_decode-gfx950-b4-gqa32x8-c1024-d256-p16-fp16",
+}
+
+
+@pytest.fixture(autouse=True)
+def _no_compilation(monkeypatch):
+    import torch.utils.cpp_extension as cpp_extension
+
+    def forbidden(*_, **__):
+        raise RuntimeError("compilation is forbidden during acceptance")
+
+    monkeypatch.setattr(cpp_extension, "load", forbidden)
+
+
+@pytest.mark.parametrize("key", sorted(ENTRY_IDS))
+def test_public_api_selects_gfx950_entry(gpu, key):
+    import radeon_kernels as rk
+    from radeon_kernels.workloads import make_inputs
+
+    data = make_inputs(key)
+    dev = to_device(data, gpu)
+    announce(f"rk.paged_attention_decode {key}")
+    out = rk.paged_attention_decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                                    dev["context_lengths"])
+    record = rk.get_last_dispatch()
+    assert record["selected"] == "native/decode_mfma", rk.explain_last_dispatch()
+    assert record["entry_id"] == ENTRY_IDS[key]
+    assert record["architecture"] == "gfx950"
+    assert "selected: native/decode_mfma" in rk.explain_last_dispatch()
+    assert_within(out, oracle64(data), data["workload"].dtype, key)
+
+
+def test_public_api_ragged_b128_selects_exact_entry(gpu):
+    import torch
+
+    import radeon_kernels as rk
+    from radeon_kernels.workloads import make_inputs
+
+    announce("rk.paged_attention_decode c5")
+    data = make_inputs("c5", device=gpu, generator_device=gpu)
+    out = rk.paged_attention_decode(data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
+                                    data["context_lengths"])
+    record = rk.get_last_dispatch()
+    assert record["selected"] == "native/decode_mfma"
+    assert record["entry_id"] == "paged_attention_decode-gfx950-b128-gqa32x8-ragged-d128-p16-bf16"
+    assert record["launch"] == {"partition_tokens": 512}
+    assert torch.isfinite(out).all().item()
+    del data
+    torch.cuda.empty_cache()
+
+
+def test_other_shapes_use_the_broad_gfx950_region(gpu):
+    import torch
+
+    import radeon_kernels as rk
+
+    case = make_case(torch, batch=3, query_heads=12, kv_heads=4, head_dim=128, block_size=32,
+                     contexts=[100, 1, 999], dtype="fp16", index_dtype="int64", seed=21)
+    dev = to_device(case, gpu)
+    announce("broad region")
+    out = rk.paged_attention_decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                                    dev["context_lengths"], 0.1)
+    record = rk.get_last_dispatch()
+    assert record["entry_id"] == "paged_attention_decode-gfx950-region"
+    assert record["selected"] == "native/decode_mfma"
+    assert_within(out, oracle64(case, scale=0.1), "fp16", "broad region")
+
+
+def test_uncovered_shape_runs_declared_fallback_exactly(gpu):
+    """block_size 48 is outside every gfx950 entry: the torch fallback runs, bit-exact to itself."""
+
+    import torch
+
+    import radeon_kernels as rk
+    from radeon_kernels.ops.paged_attention.reference import paged_attention_decode_reference
+
+    case = make_case(torch, batch=2, query_heads=8, kv_heads=2, head_dim=64, block_size=48,
+                     contexts=[57, 41], dtype="bf16", seed=8)
+    dev = to_device(case, gpu)
+    announce("uncovered shape -> fallback")
+    out = rk.paged_attention_decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                                    dev["context_lengths"])
+    expected = paged_attention_decode_reference(torch, dev["query"], dev["key_cache"], dev["value_cache"],
+                                                dev["block_tables"], dev["context_lengths"])
+    assert rk.get_last_dispatch()["selected"] == "torch/paged_attention"
+    assert torch.equal(out, expected)
+    assert_within(out, oracle64(case), "bf16", "fallback")
+
+
+def test_graph_capture_replays_match_eager(gpu):
+    import torch
+
+    import radeon_kernels as rk
+    from radeon_kernels.workloads import make_inputs
+
+    data = to_device(make_inputs("c2"), gpu)
+    args = (data["query"], data["key_cache"], data["value_cache"], data["block_tables"], data["context_lengths"])
+    announce("graph capture c2")
+    eager = rk.paged_attention_decode(*args)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            rk.paged_attention_decode(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = rk.paged_attention_decode(*args)
+    for _ in range(3):
+        scratch = torch.randn(1 << 20, device=gpu)  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+        del scratch

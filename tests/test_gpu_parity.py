@@ -1,0 +1,190 @@
+"""GPU parity: the gfx950 HIP path (through the C ABI) against the CPU oracle.
+
+Bars (max abs error against the float64 oracle on the same quantised inputs): fp16 <= 2e-3,
+bf16 <= 1.6e-2.  Every case also asserts the NaN pattern matches.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from _helpers import TOLERANCE, announce, assert_within, make_case, max_abs_error, oracle64, to_device
+from oracle import pa_oracle
+
+pytestmark = pytest.mark.gpu
+
+WORKLOAD_PARTITIONS = {"c1": 128, "c2": 64, "c3": 128, "c4": 64, "c5": 512}
+
+
+@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("key", ["c1", "c2", "c3", "c4"])
+def test_measured_workloads_match_oracle(gpu, palib, key, variant):
+    import torch
+    from radeon_kernels.workloads import make_inputs
+
+    data = make_inputs(key)  # CPU generator: bit-identical inputs everywhere
+    w = data["workload"]
+    dev = to_device(data, gpu)
+    announce(f"{key} {w.name} variant={variant}")
+    out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                       dev["context_lengths"], partition_tokens=WORKLOAD_PARTITIONS[key], variant=variant)
+    torch.cuda.synchronize()
+    expected = oracle64(data)
+    assert_within(out, expected, w.dtype, f"{key}/{variant} vs float64 oracle")
+    # The repo's own fallback algorithm in fp32 (before its final cast), evaluated on the CPU.
+    fp32 = pa_oracle.fallback_restated(torch, data["query"], data["key_cache"], data["value_cache"],
+                                       data["block_tables"], data["context_lengths"], out_dtype=torch.float32)
+    assert_within(out, fp32.numpy().astype(np.float64), w.dtype, f"{key}/{variant} vs fp32 fallback")
+
+
+@pytest.mark.parametrize("variant", ["mfma", "valu"])
+def test_ragged_b128_workload(gpu, palib, variant):
+    import torch
+    from radeon_kernels.workloads import make_inputs
+
+    announce(f"c5 ragged b128 generate on GPU, variant={variant}")
+    data = make_inputs("c5", device=gpu, generator_device=gpu)
+    out = palib.decode(data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
+                       data["context_lengths"], partition_tokens=512, variant=variant)
+    torch.cuda.synchronize()
+    ctx = data["context_lengths"].cpu().numpy()
+    order = np.argsort(ctx)
+    sample = sorted({int(order[0]), int(order[-1]), int(order[len(order) // 2]), 0, 1, 63, 127})
+    expected = pa_oracle.decode_numpy(
+        pa_oracle.as_numpy_f32(data["query"]), pa_oracle.as_numpy_f32(data["key_cache"]),
+        pa_oracle.as_numpy_f32(data["value_cache"]), data["block_tables"].cpu().numpy(), ctx,
+        accum=np.float64, sequences=sample,
+    )
+    assert_within(out[sample], expected, "bf16", f"c5/{variant} sampled rows {sample}")
+    # Size-independent properties over every row: finite, and each output is a convex
+    # combination of V rows, so it is bounded by the largest |V| of its KV head.
+    assert torch.isfinite(out).all().item()
+    bound = data["value_cache"].abs().amax().float().item()
+    assert out.abs().amax().float().item() <= bound * (1 + 2 ** -7)
+    del data
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("partition", [16, 64, 256, 1024, 8192])
+@pytest.mark.parametrize("variant", ["mfma", "valu"])
+def test_partition_sizes_agree(gpu, palib, partition, variant):
+    case = make_case(__import__("torch"), batch=4, query_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                     contexts=[1, 17, 1000, 3333], dtype="bf16", seed=11)
+    dev = to_device(case, gpu)
+    announce(f"partition={partition} variant={variant}")
+    out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                       dev["context_lengths"], partition_tokens=partition, variant=variant)
+    assert_within(out, oracle64(case), "bf16", f"partition {partition}")
+
+
+SHAPES = [
+    # (Hq, Hkv, D, BS, dtype)
+    (8, 8, 64, 16, "fp16"),
+    (16, 8, 64, 32, "bf16"),
+    (12, 4, 128, 16, "bf16"),   # group 3: one padded head slot
+    (64, 8, 128, 16, "fp16"),   # group 8: two head chunks
+    (32, 8, 256, 16, "bf16"),
+    (4, 4, 256, 8, "fp16"),
+    (32, 4, 128, 64, "bf16"),
+    (8, 2, 128, 1, "fp16"),     # one token per block
+    (6, 2, 64, 128, "bf16"),
+]
+
+
+@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_shape_sweep(gpu, palib, shape, variant):
+    import torch
+
+    hq, hkv, d, bs, dtype = shape
+    case = make_case(torch, batch=3, query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bs,
+                     contexts=[5, bs * 3 + 1, 700], dtype=dtype, seed=hq * 7 + d + bs)
+    dev = to_device(case, gpu)
+    announce(f"shape {shape} variant={variant}")
+    out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                       dev["context_lengths"], partition_tokens=128, variant=variant)
+    assert_within(out, oracle64(case), dtype, f"shape {shape}")
+
+
+def test_context_edges(gpu, palib):
+    """ctx=1 (output is that V row), block boundaries, full table, over-long and empty contexts."""
+
+    import torch
+
+    bs, mb = 16, 6
+    contexts = [1, bs, bs + 1, mb * bs, mb * bs + 40, 0, -3]
+    case = make_case(torch, batch=len(contexts), query_heads=8, kv_heads=2, head_dim=128, block_size=bs,
+                     contexts=contexts, max_blocks=mb, dtype="fp16", seed=5)
+    dev = to_device(case, gpu)
+    announce("context edges")
+    for partition in (16, 64, 4096):
+        out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                           dev["context_lengths"], partition_tokens=partition).cpu()
+        assert_within(out, oracle64(case), "fp16", f"edges partition {partition}")
+        assert torch.isnan(out[5]).all() and torch.isnan(out[6]).all()
+        # ctx = 1: softmax weight 1 on token 0, so the output is exactly token 0's V row.
+        block0 = int(case["block_tables"][0, 0])
+        for h in range(8):
+            assert torch.equal(out[0, h], case["value_cache"][block0, 0, h // 4])
+
+
+def test_int64_indices_and_explicit_scale(gpu, palib):
+    import torch
+
+    case = make_case(torch, batch=2, query_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                     contexts=[300, 77], dtype="bf16", index_dtype="int64", seed=9)
+    dev = to_device(case, gpu)
+    announce("int64 indices, scale 0.05")
+    out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                       dev["context_lengths"], 0.05, partition_tokens=64)
+    assert_within(out, oracle64(case, scale=0.05), "bf16", "int64/explicit scale")
+
+
+def test_out_of_range_block_ids_are_skipped(gpu, palib):
+    import torch
+
+    case = make_case(torch, batch=1, query_heads=8, kv_heads=2, head_dim=64, block_size=16,
+                     contexts=[64], dtype="fp16", seed=3)
+    num_blocks = case["key_cache"].shape[0]
+    bad = case["block_tables"].clone()
+    bad[0, 1] = num_blocks + 1000   # tokens 16..31 point outside the cache
+    bad[0, 2] = -1                  # tokens 32..47 likewise
+    dev = to_device(case, gpu)
+    announce("out-of-range block ids")
+    out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], bad.to(gpu),
+                       dev["context_lengths"], partition_tokens=16)
+    # Same as attending only over the valid tokens: blocks 0 and 3 (tokens 0-15, 48-63).
+    keep = case["block_tables"][0, [0, 3]]
+    compact = dict(case)
+    compact["block_tables"] = keep.view(1, 2).to(case["block_tables"].dtype)
+    compact["context_lengths"] = torch.tensor([32], dtype=case["context_lengths"].dtype)
+    assert_within(out, oracle64(compact), "fp16", "skipped blocks")
+
+
+def test_non_finite_propagates(gpu, palib):
+    import torch
+
+    case = make_case(torch, batch=2, query_heads=8, kv_heads=2, head_dim=128, block_size=16,
+                     contexts=[40, 40], dtype="bf16", seed=4)
+    block = int(case["block_tables"][0, 1])
+    case["key_cache"][block, 3, 1, 7] = float("nan")  # sequence 0, token 19, KV head 1
+    dev = to_device(case, gpu)
+    announce("NaN in K")
+    out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
+                       dev["context_lengths"], partition_tokens=16).cpu()
+    assert torch.isnan(out[0, 4:8]).all()          # query heads of KV head 1
+    assert torch.isfinite(out[0, 0:4]).all() and torch.isfinite(out[1]).all()
+
+
+def test_deterministic(gpu, palib):
+    import torch
+    from radeon_kernels.workloads import make_inputs
+
+    data = to_device(make_inputs("c2"), gpu)
+    announce("determinism c2")
+    runs = [palib.decode(data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
+                         data["context_lengths"], partition_tokens=64) for _ in range(3)]
+    assert all(torch.equal(runs[0], r) for r in runs[1:])

@@ -1,0 +1,276 @@
+#!/usr/bin/env python3
+"""Paged-attention decode benchmark on one MI355X (gfx950).
+
+One step = one decode call (partition kernel + partition-reduce kernel) over the whole batch of the
+workload, inputs resident in HBM.  Default workload: 128 sequences, 32 query / 8 KV heads, head_dim
+128, block 16, bf16, context lengths ~ U[1024, 16384] (seeded), about 4.8 GB of K/V per call -- 18x
+the 256 MB last-level cache, so every call streams from HBM.
+
+Prints one JSON line:
+  value            effective KV GB/s = algorithmic K+V bytes per call / wall time per call
+  us_per_call      wall time per call (both kernels, back-to-back launches)
+  roofline         the partition kernel against the 8 TB/s HBM peak: achieved = KV bytes / its
+                   average duration, timed with HIP events recorded on the launch stream around
+                   each phase inside the timed region; traffic = measured HBM bytes per launch
+                   from the committed rocprofv3 counter summary for this exact configuration
+                   (null when there is none)
+  cpu_baseline     the reference algorithm (its torch fallback, restated in oracle/) on the host
+                   cores over a bounded sample of the same workload
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5] [--variant mfma]
+                       [--partition P] [--no-cpu-baseline] [--cpu-seconds S] [--calibration-copy]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for entry in (str(ROOT / "radeon-kernels_amd"), str(ROOT)):
+    if entry not in sys.path:
+        sys.path.insert(0, entry)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "paged-attn decode µs/call + effective KV GB/s (% MI355X HBM peak), b128"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "pa_partition_kernel_b128_traffic.txt"
+
+
+def parse_args(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--variant", default=None, choices=["mfma", "valu"])
+    parser.add_argument("--partition", type=int, default=None)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--calibration-copy", action="store_true",
+                        help="run a 1 GiB device copy before timing (counter calibration under rocprofv3)")
+    return parser.parse_args(argv)
+
+
+def dispatch_launch(workload_key: str) -> tuple[str, int]:
+    """Entrypoint and partition size the gfx950 dispatch table assigns to this workload."""
+
+    from radeon_kernels import dispatch_plan
+
+    names = {"c1": "b1-gqa32x8-c128-d128-p16-fp16", "c2": "b8-gqa32x8-c1024-d128-p16-bf16",
+             "c3": "b4-mha16-c2048-d64-p32-bf16", "c4": "b4-gqa32x8-c1024-d256-p16-fp16",
+             "c5": "b128-gqa32x8-ragged-d128-p16-bf16"}
+    for suffix, _, launch in dispatch_plan.EXACT_REGIONS:
+        if suffix == names[workload_key]:
+            return dispatch_plan.ENTRYPOINT, int(launch["partition_tokens"])
+    raise KeyError(workload_key)
+
+
+def read_traffic(workload: str, variant: str, partition: int):
+    """HBM bytes per partition-kernel launch from the committed counter summary, if it matches."""
+
+    if not TRAFFIC_SUMMARY.is_file():
+        return None
+    fields = {}
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if "=" in line and not line.lstrip().startswith("#"):
+            key, value = line.split("=", 1)
+            fields[key.strip()] = value.strip()
+    try:
+        if fields.get("workload") != workload or fields.get("variant") != variant or int(fields["partition_tokens"]) != partition:
+            return None
+        return int(fields["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(torch, data, seconds: float) -> dict:
+    """Reference algorithm on the host cores over the first sequences of the workload."""
+
+    from oracle import pa_oracle
+
+    threads = torch.get_num_threads()
+    w = data["workload"]
+    bt_all = data["block_tables"].cpu().to(torch.int64)
+    ctx_all = data["context_lengths"].cpu().to(torch.int64)
+    batch = bt_all.shape[0]
+    done, elapsed, kv_done, tokens_done = 0, 0.0, 0, 0
+    chunk = 2
+    while done < batch and elapsed < seconds:
+        rows = list(range(done, min(batch, done + chunk)))
+        bt = bt_all[rows]
+        ctx = ctx_all[rows]
+        need = [min(math.ceil(int(c) / w.block_size), w.max_blocks) for c in ctx]
+        used = torch.cat([bt[i, : need[i]] for i in range(len(rows))])
+        remap = {int(b): i for i, b in enumerate(used.tolist())}
+        compact = torch.zeros_like(bt)
+        for i in range(len(rows)):
+            compact[i, : need[i]] = torch.tensor([remap[int(b)] for b in bt[i, : need[i]]])
+        index = used.to(data["key_cache"].device)
+        k = data["key_cache"].index_select(0, index).cpu()
+        v = data["value_cache"].index_select(0, index).cpu()
+        q = data["query"][rows].cpu()
+        start = time.perf_counter()
+        pa_oracle.fallback_restated(torch, q, k, v, compact.to(torch.int32), ctx.to(torch.int32))
+        elapsed += time.perf_counter() - start
+        done += len(rows)
+        tokens_done += int(sum(min(int(c), w.max_blocks * w.block_size) for c in ctx))
+    kv_done = tokens_done * w.kv_heads * w.head_dim * 2 * w.elem_size
+    gbps = kv_done / elapsed / 1e9
+    return {
+        "value": round(gbps, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"first {done} of {batch} sequences ({tokens_done} context tokens, {kv_done / 1e9:.3f} GB of K/V), "
+                   f"evaluated {chunk} sequences at a time by the reference's torch fallback restated in "
+                   f"oracle/pa_oracle.py (torch {torch.__version__} CPU, {threads} threads), {elapsed:.1f} s"),
+        "us_per_call_extrapolated": round(data["kv_bytes"] / (gbps * 1e9) * 1e6, 1),
+    }
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only; the decode shards by sequence and KV head "
+                          "with no exchange, so multi-GPU throughput is N x the single-GPU value and is not measured here",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import torch
+
+    from radeon_kernels.cabi import library
+    from radeon_kernels.workloads import WORKLOADS, make_inputs
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no visible ROCm GPU"}))
+        return 1
+    device = torch.device("cuda:0")
+    arch = torch.cuda.get_device_properties(0).gcnArchName.split(":", 1)[0]
+    lib = library()  # raises if the HIP library was not built
+    w = WORKLOADS[args.workload]
+    entrypoint, planned_partition = dispatch_launch(args.workload)
+    variant = args.variant or entrypoint.split("_", 1)[1]
+    partition = args.partition or planned_partition
+
+    if args.calibration_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    data = make_inputs(w, device=device, generator_device=device if w.ragged else "cpu")
+    kv_bytes = data["kv_bytes"]
+    cache_bytes = data["key_cache"].numel() * 2 * 2
+    # Small workloads fit in the 256 MB last-level cache: rotate among enough K/V copies that each
+    # call reads its cache from HBM.
+    copies = 1 if w.ragged else max(16, math.ceil(768e6 / cache_bytes))
+    caches = [(data["key_cache"], data["value_cache"])]
+    for _ in range(copies - 1):
+        caches.append((data["key_cache"].clone(), data["value_cache"].clone()))
+    q, bt, cl = data["query"], data["block_tables"], data["context_lengths"]
+    batch, hq, d = q.shape
+    nb, bs, hkv, _ = data["key_cache"].shape
+    mb = bt.shape[1]
+    need = lib.workspace_bytes(batch, hq, d, bs, mb, partition)
+    out = torch.empty_like(q)
+    workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device)
+
+    def launch(phase: str, k, v):
+        lib.decode(q, k, v, bt, cl, partition_tokens=partition, variant=variant, out=out, workspace=workspace,
+                   stream=stream, phase=phase)
+
+    for i in range(args.warmup):
+        k, v = caches[i % copies]
+        launch("partitions", k, v)
+        launch("reduce", k, v)
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        k, v = caches[i % copies]
+        ev = events[i]
+        ev[0].record(stream)
+        launch("partitions", k, v)
+        ev[1].record(stream)
+        launch("reduce", k, v)
+        ev[2].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    part_us = [e[0].elapsed_time(e[1]) * 1e3 for e in events]
+    red_us = [e[1].elapsed_time(e[2]) * 1e3 for e in events]
+    us_per_call = wall / args.steps * 1e6
+    gbps = kv_bytes / (us_per_call * 1e3)
+    part_avg = statistics.fmean(part_us)
+    achieved = kv_bytes / (part_avg * 1e3)
+
+    hot = None
+    if copies > 1:  # the same cache every call: last-level-cache resident
+        k, v = caches[0]
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(args.steps):
+            launch("all", k, v)
+        torch.cuda.synchronize()
+        hot = round((time.perf_counter() - t) / args.steps * 1e6, 2)
+
+    traffic = read_traffic(w.name, variant, partition)
+    result = {
+        "metric": METRIC,
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic (seeded N(0,1) query/K/V, seeded block tables and context lengths)",
+        "config": {
+            "workload": w.name,
+            "batch": int(batch), "query_heads": int(hq), "kv_heads": int(hkv), "head_dim": int(d),
+            "block_size": int(bs), "num_blocks": int(nb), "max_blocks_per_sequence": int(mb),
+            "context": list(w.context) if w.ragged else w.context, "seed": data["seed"],
+            "entrypoint": f"decode_{variant}", "partition_tokens": partition, "kv_copies_rotated": copies,
+            "arch": arch,
+        },
+        "us_per_call": round(us_per_call, 2),
+        "pct_hbm_peak": round(gbps / HBM_PEAK_GBPS * 100, 2),
+        "kv_bytes_per_call": kv_bytes,
+        "kernels_us": {
+            "pa_partition_kernel": {"avg": round(part_avg, 2), "min": round(min(part_us), 2), "max": round(max(part_us), 2)},
+            "pa_reduce_kernel": {"avg": round(statistics.fmean(red_us), 2), "min": round(min(red_us), 2),
+                                 "max": round(max(red_us), 2)},
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+        },
+    }
+    if hot is not None:
+        result["us_per_call_cache_resident"] = hot
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, data, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -92,6 +92,30 @@ int rk_pa_decode(const void* query, const void* key_cache, const void* value_cac
                  int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
                  int64_t partition_tokens, int variant, void* stream);
 
+/*
+ * The two launches rk_pa_decode makes, callable separately with the same arguments (no reference
+ * counterpart; the reference kernel is a single pass).  rk_pa_decode_partitions runs the split-K
+ * partition kernel: it writes the final output of every sequence that fits in one partition and a
+ * partial record of every other partition into the workspace.  rk_pa_decode_reduce then merges
+ * those records into the output (it launches nothing when one partition covers
+ * max_blocks_per_sequence * block_size).  Issued in that order on one stream they are exactly
+ * rk_pa_decode; splitting them lets a caller time or schedule the phases individually.
+ */
+int rk_pa_decode_partitions(const void* query, const void* key_cache, const void* value_cache,
+                            const void* block_tables, const void* context_lengths, void* output,
+                            void* workspace, size_t workspace_bytes, int64_t batch,
+                            int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                            int64_t num_blocks, int64_t block_size,
+                            int64_t max_blocks_per_sequence, float scale, int dtype,
+                            int index_dtype, int64_t partition_tokens, int variant, void* stream);
+int rk_pa_decode_reduce(const void* query, const void* key_cache, const void* value_cache,
+                        const void* block_tables, const void* context_lengths, void* output,
+                        void* workspace, size_t workspace_bytes, int64_t batch,
+                        int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                        int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_sequence,
+                        float scale, int dtype, int index_dtype, int64_t partition_tokens,
+                        int variant, void* stream);
+
 /* Text describing the last non-RK_OK status returned on the calling thread. */
 const char* rk_pa_last_error(void);
 

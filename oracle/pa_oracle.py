@@ -194,7 +194,8 @@ def round_to_bf16(x: np.ndarray) -> np.ndarray:
 
 
 def round_to_fp16(x: np.ndarray) -> np.ndarray:
-    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    with np.errstate(over="ignore"):  # values past 65504 round to inf, as the cast defines
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
 def round_to(x: np.ndarray, dtype: str) -> np.ndarray:

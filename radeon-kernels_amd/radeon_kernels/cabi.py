@@ -29,7 +29,15 @@ RK_INDEX_INT32 = 0
 RK_INDEX_INT64 = 1
 VARIANTS = {"mfma": 0, "valu": 1}
 
-EXPORTED_SYMBOLS = ("rk_pa_decode", "rk_pa_decode_workspace_bytes", "rk_pa_last_error", "rk_pa_version")
+EXPORTED_SYMBOLS = (
+    "rk_pa_decode",
+    "rk_pa_decode_partitions",
+    "rk_pa_decode_reduce",
+    "rk_pa_decode_workspace_bytes",
+    "rk_pa_last_error",
+    "rk_pa_version",
+)
+PHASES = {"all": "rk_pa_decode", "partitions": "rk_pa_decode_partitions", "reduce": "rk_pa_decode_reduce"}
 
 
 class CabiError(RuntimeError):
@@ -51,9 +59,11 @@ class PagedAttentionLibrary:
         i64, vp, sz = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
         lib.rk_pa_decode_workspace_bytes.argtypes = [i64, i64, i64, i64, i64, i64, ctypes.POINTER(sz)]
         lib.rk_pa_decode_workspace_bytes.restype = ctypes.c_int
-        lib.rk_pa_decode.argtypes = [vp, vp, vp, vp, vp, vp, vp, sz, i64, i64, i64, i64, i64, i64, i64,
-                                     ctypes.c_float, ctypes.c_int, ctypes.c_int, i64, ctypes.c_int, vp]
-        lib.rk_pa_decode.restype = ctypes.c_int
+        decode_args = [vp, vp, vp, vp, vp, vp, vp, sz, i64, i64, i64, i64, i64, i64, i64,
+                       ctypes.c_float, ctypes.c_int, ctypes.c_int, i64, ctypes.c_int, vp]
+        for symbol in PHASES.values():
+            getattr(lib, symbol).argtypes = decode_args
+            getattr(lib, symbol).restype = ctypes.c_int
         lib.rk_pa_last_error.argtypes = []
         lib.rk_pa_last_error.restype = ctypes.c_char_p
         lib.rk_pa_version.argtypes = []
@@ -80,15 +90,16 @@ class PagedAttentionLibrary:
     def decode_raw(self, *, query: int, key_cache: int, value_cache: int, block_tables: int, context_lengths: int,
                    output: int, workspace: int, workspace_bytes: int, batch: int, query_heads: int, kv_heads: int,
                    head_dim: int, num_blocks: int, block_size: int, max_blocks: int, scale: float, dtype: int,
-                   index_dtype: int, partition_tokens: int, variant: int, stream: int) -> int:
-        return self.lib.rk_pa_decode(query, key_cache, value_cache, block_tables, context_lengths, output,
+                   index_dtype: int, partition_tokens: int, variant: int, stream: int, phase: str = "all") -> int:
+        return getattr(self.lib, PHASES[phase])(query, key_cache, value_cache, block_tables, context_lengths, output,
                                      workspace or None, workspace_bytes, batch, query_heads, kv_heads, head_dim,
                                      num_blocks, block_size, max_blocks, ctypes.c_float(scale), dtype, index_dtype,
                                      partition_tokens, variant, stream or None)
 
     def decode(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
                scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
-               out: Any | None = None, workspace: Any | None = None, stream: Any | None = None) -> Any:
+               out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
+               phase: str = "all") -> Any:
         """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None)."""
 
         import torch
@@ -113,7 +124,7 @@ class PagedAttentionLibrary:
             block_size=block_size, max_blocks=max_blocks, scale=float(scale),
             dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
             index_dtype=RK_INDEX_INT64 if block_tables.dtype == torch.int64 else RK_INDEX_INT32,
-            partition_tokens=partition_tokens, variant=VARIANTS[variant], stream=stream.cuda_stream,
+            partition_tokens=partition_tokens, variant=VARIANTS[variant], stream=stream.cuda_stream, phase=phase,
         )
         self.check(status)
         return out

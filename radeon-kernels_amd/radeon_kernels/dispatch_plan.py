@@ -60,7 +60,7 @@ EXACT_REGIONS: list[tuple[str, dict[str, Any], dict[str, Any]]] = [
         "b128-gqa32x8-ragged-d128-p16-bf16",
         {"dtype": "bf16", "batch": 128, "query_heads": 32, "kv_heads": 8, "head_dim": 128,
          "num_blocks": [1, _INT_MAX], "block_size": 16, "max_blocks_per_sequence": 1024},
-        {"partition_tokens": 512},
+        {"partition_tokens": 2048},
     ),
 ]
 

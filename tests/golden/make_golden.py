@@ -1,0 +1,118 @@
+"""Regenerate the committed paged-attention fixtures in this directory.
+
+    python tests/golden/make_golden.py
+
+Writes:
+  tiny_cases.npz   small decode cases (inputs as raw 16-bit patterns, float64 expected outputs from
+                   the token-by-token brute force in oracle/pa_oracle.py, and those outputs rounded
+                   to the storage dtype).  Shapes include the reference's fallback-acceptance case
+                   (developer/promotion/verify_paged_attention_fallback.py:43-47: B=2, Hq=8, Hkv=2,
+                   D=64, block 16, tables [[3,1,6,0],[7,2,5,4]], contexts [57,41]) and the context
+                   boundaries 1, block_size, block_size+1.
+  c1_expected.npz  the 1-sequence 32/8-head d128 fp16 workload: SHA-256 of each seeded input
+                   tensor, float64 brute-force output and its fp16 rounding.
+  reference_dispatch_paged_attention_decode-1.0.json
+                   the reference's published paged-attention dispatch manifest (data, Apache-2.0),
+                   used to prove the gfx950 entries merge into it; copied from /root/reference when
+                   that tree is present.
+
+The reference repository holds no numeric vectors for this operator; these are produced by the
+oracle's brute force, which the tests pin independently (closed forms, library SDPA, invariants).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+for entry in (str(ROOT), str(ROOT / "radeon-kernels_amd")):
+    if entry not in sys.path:
+        sys.path.insert(0, entry)
+
+from oracle import pa_oracle  # noqa: E402
+
+TINY_CASES = [
+    # name, B, Hq, Hkv, D, BS, tables, contexts, dtype, seed
+    ("acceptance_fp16", 2, 8, 2, 64, 16, [[3, 1, 6, 0], [7, 2, 5, 4]], [57, 41], "fp16", 20261000),
+    ("acceptance_bf16", 2, 8, 2, 64, 16, [[3, 1, 6, 0], [7, 2, 5, 4]], [57, 41], "bf16", 20261001),
+    ("boundaries_bf16", 3, 4, 1, 64, 16, [[5, 2], [0, 7], [3, 6]], [1, 16, 17], "bf16", 20261002),
+    ("gqa4_d128_fp16", 1, 8, 2, 128, 8, [[4, 0, 2]], [20], "fp16", 20261003),
+    ("mha_d256_bf16", 2, 2, 2, 256, 4, [[1, 3], [2, 0]], [7, 5], "bf16", 20261004),
+]
+
+
+def tensor_bits(tensor) -> np.ndarray:
+    import torch
+
+    return tensor.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def sha256_tensor(tensor) -> str:
+    return hashlib.sha256(tensor.contiguous().view(-1).view(__import__("torch").uint8).numpy().tobytes()).hexdigest()
+
+
+def tiny_case_inputs(torch, b, hq, hkv, d, bs, tables, contexts, dtype, seed):
+    num_blocks = max(max(row) for row in tables) + 1
+    gen = torch.Generator().manual_seed(seed)
+    dt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    query = torch.randn((b, hq, d), generator=gen).to(dt)
+    key = torch.randn((num_blocks, bs, hkv, d), generator=gen).to(dt)
+    value = torch.randn((num_blocks, bs, hkv, d), generator=gen).to(dt)
+    return query, key, value, torch.tensor(tables, dtype=torch.int32), torch.tensor(contexts, dtype=torch.int32)
+
+
+def brute(query, key, value, tables, contexts) -> np.ndarray:
+    f = pa_oracle.as_numpy_f32
+    return np.asarray(pa_oracle.decode_bruteforce(f(query).tolist(), f(key).tolist(), f(value).tolist(),
+                                                  tables.tolist(), contexts.tolist()), dtype=np.float64)
+
+
+def main() -> None:
+    import torch
+
+    arrays: dict[str, np.ndarray] = {}
+    for name, b, hq, hkv, d, bs, tables, contexts, dtype, seed in TINY_CASES:
+        q, k, v, bt, cl = tiny_case_inputs(torch, b, hq, hkv, d, bs, tables, contexts, dtype, seed)
+        expected = brute(q, k, v, bt, cl)
+        arrays[f"{name}/query"] = tensor_bits(q)
+        arrays[f"{name}/key_cache"] = tensor_bits(k)
+        arrays[f"{name}/value_cache"] = tensor_bits(v)
+        arrays[f"{name}/block_tables"] = bt.numpy()
+        arrays[f"{name}/context_lengths"] = cl.numpy()
+        arrays[f"{name}/dtype"] = np.array(dtype)
+        arrays[f"{name}/expected_f64"] = expected
+        arrays[f"{name}/expected_rounded"] = pa_oracle.round_to(expected.astype(np.float32), dtype)
+    np.savez_compressed(HERE / "tiny_cases.npz", **arrays)
+
+    from radeon_kernels.workloads import make_inputs
+
+    data = make_inputs("c1")
+    expected = brute(data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
+                     data["context_lengths"])
+    np.savez_compressed(
+        HERE / "c1_expected.npz",
+        sha_query=np.array(sha256_tensor(data["query"])),
+        sha_key_cache=np.array(sha256_tensor(data["key_cache"])),
+        sha_value_cache=np.array(sha256_tensor(data["value_cache"])),
+        sha_block_tables=np.array(sha256_tensor(data["block_tables"])),
+        sha_context_lengths=np.array(sha256_tensor(data["context_lengths"])),
+        expected_f64=expected,
+        expected_fp16=pa_oracle.round_to_fp16(expected.astype(np.float32)),
+    )
+
+    source = Path("/root/reference/dispatch/paged_attention_decode-1.0.json")
+    if source.is_file():
+        document = json.loads(source.read_text(encoding="utf-8"))
+        (HERE / "reference_dispatch_paged_attention_decode-1.0.json").write_text(
+            json.dumps(document, indent=1, sort_keys=True) + "\n", encoding="utf-8")
+    print("fixtures written to", HERE)
+
+
+if __name__ == "__main__":
+    main()

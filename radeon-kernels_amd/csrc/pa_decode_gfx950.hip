@@ -47,6 +47,9 @@ constexpr int kThreads = kWave * kWaves;
 constexpr int kTile = 16;             // tokens per wave step = MFMA M
 constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, plus one straddle
 constexpr float kLog2e = 1.4426950408889634f;
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 only: vmcnt bits [3:0] and [15:14]
+// zero, expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait on those counters).
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -133,9 +136,21 @@ __device__ __forceinline__ float row_sum16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// global_load_lds_dwordx4: each lane's 16 bytes at `src` land in LDS at `lds_base` + 16 * lane
+// (lds_base must be wave-uniform).  Completion is tracked by the wave's memory counter.  Kept in a
+// device function so the host compilation pass never sees the target builtin.
+__device__ __forceinline__ void dma_to_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
+
 template <bool B>
 struct Flag {
   static constexpr bool value = B;
+};
+
+template <int N>
+struct Int {
+  static constexpr int value = N;
 };
 
 __device__ __forceinline__ int64_t load_index(const void* base, int64_t i, bool is64) {
@@ -183,24 +198,44 @@ __device__ __forceinline__ int64_t clamped_context(const Params& p, int b) {
 //   QK_MFMA QK^T on MFMA (true) or on fp32 FMAs + DPP row sums (false)
 //   UB      block_size >= 16: every 16-aligned tile lies inside one cache block, so the block id is
 //           wave-uniform and addresses are a scalar base plus fixed 32-bit per-lane offsets
+//
+// MFMA variant data path per 16-token tile and wave:
+//   K: global_load_lds_dwordx4 straight into a per-wave LDS slot (two slots, double buffered).
+//      Each DMA instruction moves whole cache rows (coalesced); lane l fetches chunk
+//      (l % CPR) ^ (row & SWZ) of its row, so the hardware's lane-contiguous LDS write leaves the
+//      tile XOR-swizzled and the MFMA operand read (token j, chunk 4i+g) is bank-conflict free.
+//   V: 16-byte register loads, one token row per 16-lane group (rows 4g..4g+3).
+//   Order: read K(n) from LDS -> MFMA -> issue K(n+1) DMA and V(n+1) loads -> softmax -> PV(n).
 template <class E, int D, int GC, bool QK_MFMA, bool UB>
 __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
-  constexpr int KSTEPS = D / 32;  // MFMA k-steps (16-byte K chunks per lane per tile)
-  constexpr int VEC = D / 16;     // elements of a token row per lane (row = 16 lanes)
-  constexpr int VW = VEC / 2;     // 32-bit words per lane per token row
+  constexpr int KSTEPS = D / 32;       // MFMA k-steps; also DMA instructions per K tile
+  constexpr int VEC = D / 16;          // elements of a token row per lane (row = 16 lanes)
+  constexpr int VW = VEC / 2;          // 32-bit words per lane per token row
+  constexpr int CPR = D / 8;           // 16-byte chunks per cache row (one token, one KV head)
+  constexpr int RPI = kWave / CPR;     // cache rows per DMA instruction
+  constexpr int SWZ = CPR - 1 < 15 ? CPR - 1 : 15;  // chunk swizzle mask
+  constexpr int KTILE16 = kTile * CPR; // 16-byte units of one staged K tile
   static_assert(GC == 1 || GC == 2 || GC == 4, "head chunk must be 1, 2 or 4");
   static_assert(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
+  static_assert(KTILE16 == KSTEPS * kWave, "one DMA instruction per MFMA k-step");
 
+  // The K staging slots and, after the main loop, the per-wave partial accumulators share one
+  // LDS buffer (a barrier separates the two uses).
+  constexpr int K_STAGE_BYTES = QK_MFMA ? kWaves * 2 * KTILE16 * 16 : 0;
+  constexpr int ACC_BYTES = kWaves * GC * D * 4;
+  constexpr int RAW_BYTES = K_STAGE_BYTES > ACC_BYTES ? K_STAGE_BYTES : ACC_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char s_raw[RAW_BYTES];
   __shared__ int s_table[kMaxSliceBlocks];
-  __shared__ float s_acc[kWaves][GC][D];
   __shared__ float s_m[kWaves][GC];
   __shared__ float s_l[kWaves][GC];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4;   // lane group: owns tokens 4g..4g+3 of every tile (V / scores)
   const int j = lane & 15;   // lane in group: token j of the tile for K (MFMA), V column block
+  u32x4* const s_k = reinterpret_cast<u32x4*>(s_raw) + wave * 2 * KTILE16;
+  float(*const s_acc)[GC][D] = reinterpret_cast<float(*)[GC][D]>(s_raw);
 
   // Workgroup -> (partition, sequence, KV head, head chunk), KV head / chunk varying fastest and
   // partition slowest.  The workgroups of all KV heads of one token range are dispatched together,
@@ -281,73 +316,66 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   const uint16_t* __restrict__ vbase = p.v + static_cast<int64_t>(kvh) * D;
 
   struct Tile {
-    u32x4 k[QK_MFMA ? KSTEPS : 1];
-    uint32_t kr[QK_MFMA ? 1 : 4][QK_MFMA ? 1 : VW];
+    uint32_t kr[QK_MFMA ? 1 : 4][QK_MFMA ? 1 : VW];  // VALU variant: K rows like V
     uint32_t v[4][VW];
     uint32_t valid;  // bit r: token t0 + 4g + r is inside the partition and its block is valid
     bool full;       // wave-uniform: all 16 tokens valid (no masking needed)
   };
 
   // Loads are unconditional and always in bounds: a token past the partition end, or one whose
-  // block id is invalid, reads a row of block 0 instead and its data is discarded after the load
-  // (score -> -inf, V row -> 0).  Branch-free loads keep the wave's memory counter exact, so the
-  // next tile's loads stay in flight while the current tile is consumed.  With block_size >= 16
-  // a 16-aligned tile lies inside one block and one table lookup serves the whole wave.
+  // block id is invalid, reads a row of block 0 (or of the tile's block) instead and its data is
+  // discarded after the load (score -> -inf, V row -> 0).  Branch-free loads keep the wave's
+  // memory counter exact, so the next tile's loads stay in flight while the current one is used.
   const int last = p_end - 1;
-  const bool uniform_block = p.bs_log2 >= 4;
   auto block_of = [&](int t) -> int { return s_table[(min(t, last) >> lb) - blk0]; };
   auto row_base = [&](int pb, int t) -> int64_t {
     return static_cast<int64_t>(pb < 0 ? 0 : pb) * p.block_stride +
            static_cast<int64_t>(t & bs_mask) * p.row_stride;
   };
 
-  // Per-lane element offsets of a tile's rows relative to its first token (uniform-block path);
-  // the host guarantees 16 * row_stride fits in 31 bits.
+  // Per-lane element offsets relative to a tile's first row (uniform-block path); the host
+  // guarantees 16 * row_stride fits in 31 bits.
   const int32_t row_stride32 = static_cast<int32_t>(p.row_stride);
-  const int32_t k_lane_off = j * row_stride32 + g * 8;
   int32_t v_lane_off[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) v_lane_off[r] = (4 * g + r) * row_stride32 + j * VEC;
-
-  auto load_rows = [&](Tile& tile, const uint16_t* kb_lane, const uint16_t* const vb_lane[4]) {
-    if constexpr (QK_MFMA) {
+  const int dma_row = lane / CPR;  // row (within RPI) a lane moves in each K DMA instruction
+  const int dma_pos = lane % CPR;  // its 16-byte position in the staged row
+  int32_t kdma_off[QK_MFMA ? KSTEPS : 1];
+  int kread[QK_MFMA ? KSTEPS : 1];
+  if constexpr (QK_MFMA) {
 #pragma unroll
-      for (int i = 0; i < KSTEPS; ++i) tile.k[i] = *reinterpret_cast<const u32x4*>(kb_lane + i * 32);
+    for (int n = 0; n < KSTEPS; ++n) {
+      const int row = RPI * n + dma_row;
+      kdma_off[n] = row * row_stride32 + ((dma_pos ^ (row & SWZ)) << 3);
     }
+#pragma unroll
+    for (int i = 0; i < KSTEPS; ++i) kread[i] = j * CPR + ((4 * i + g) ^ (j & SWZ));
+  }
+
+  auto load_v_rows = [&](uint32_t (&dst)[4][VW], const uint16_t* const src[4]) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       if constexpr (VW == 2) {
-        const u32x2 x = *reinterpret_cast<const u32x2*>(vb_lane[r]);
-        tile.v[r][0] = x[0];
-        tile.v[r][1] = x[1];
+        const u32x2 x = *reinterpret_cast<const u32x2*>(src[r]);
+        dst[r][0] = x[0];
+        dst[r][1] = x[1];
       } else {
 #pragma unroll
         for (int w4 = 0; w4 < VW / 4; ++w4) {
-          const u32x4 x = *reinterpret_cast<const u32x4*>(vb_lane[r] + w4 * 8);
+          const u32x4 x = *reinterpret_cast<const u32x4*>(src[r] + w4 * 8);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) tile.v[r][w4 * 4 + e] = x[e];
-        }
-      }
-      if constexpr (!QK_MFMA) {
-        // K rows of masked tokens need no zeroing: their scores are replaced by -inf.
-        const uint16_t* ksrc = vb_lane[r] - vbase + kbase;
-        if constexpr (VW == 2) {
-          const u32x2 x = *reinterpret_cast<const u32x2*>(ksrc);
-          tile.kr[r][0] = x[0];
-          tile.kr[r][1] = x[1];
-        } else {
-#pragma unroll
-          for (int w4 = 0; w4 < VW / 4; ++w4) {
-            const u32x4 x = *reinterpret_cast<const u32x4*>(ksrc + w4 * 8);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) tile.kr[r][w4 * 4 + e] = x[e];
-          }
+          for (int e = 0; e < 4; ++e) dst[r][w4 * 4 + e] = x[e];
         }
       }
     }
   };
 
-  auto load_tile = [&](Tile& tile, int t0) {
+  // Issue every load of the tile starting at token t0: K into LDS slot `slot` (MFMA variant) or
+  // registers (VALU variant), V into registers.
+  auto issue_tile = [&](Tile& tile, int slot, int t0) {
+    const uint16_t* vrow[4];
+    const uint16_t* krow[4];
     if constexpr (UB) {
       const int pb = __builtin_amdgcn_readfirstlane(s_table[(t0 >> lb) - blk0]);
       const bool block_ok = pb >= 0;
@@ -357,24 +385,42 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
       tile.valid = 0;
 #pragma unroll
       for (int r = 0; r < 4; ++r) tile.valid |= (block_ok && t0 + 4 * g + r < p_end) ? (1u << r) : 0u;
-      const uint16_t* vb = vbase + base;
-      const uint16_t* const vb_lane[4] = {vb + v_lane_off[0], vb + v_lane_off[1], vb + v_lane_off[2],
-                                          vb + v_lane_off[3]};
-      load_rows(tile, kbase + base + k_lane_off, vb_lane);
+      if constexpr (QK_MFMA) {
+        const uint16_t* kb = kbase + base;
+        u32x4* dst = s_k + slot * KTILE16;
+#pragma unroll
+        for (int n = 0; n < KSTEPS; ++n)
+          dma_to_lds16(kb + kdma_off[n], dst + n * kWave);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        vrow[r] = vbase + base + v_lane_off[r];
+        krow[r] = kbase + base + v_lane_off[r];
+      }
     } else {
-      const int pbk = block_of(t0 + j);
-      const uint16_t* vb_lane[4];
+      tile.full = false;
       tile.valid = 0;
+      if constexpr (QK_MFMA) {
+        u32x4* dst = s_k + slot * KTILE16;
+#pragma unroll
+        for (int n = 0; n < KSTEPS; ++n) {
+          const int row = RPI * n + dma_row;
+          const int t = t0 + row;
+          const uint16_t* src = kbase + row_base(block_of(t), t) + ((dma_pos ^ (row & SWZ)) << 3);
+          dma_to_lds16(src, dst + n * kWave);
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = t0 + 4 * g + r;
         const int pb = block_of(t);
         tile.valid |= (t < p_end && pb >= 0) ? (1u << r) : 0u;
-        vb_lane[r] = vbase + row_base(pb, t) + j * VEC;
+        vrow[r] = vbase + row_base(pb, t) + j * VEC;
+        krow[r] = kbase + row_base(pb, t) + j * VEC;
       }
-      tile.full = false;
-      load_rows(tile, kbase + row_base(pbk, t0 + j) + g * 8, vb_lane);
     }
+    if constexpr (!QK_MFMA) load_v_rows(tile.kr, krow);  // K rows of masked tokens need no zeroing
+    load_v_rows(tile.v, vrow);
   };
 
   // Online-softmax state.  m_own / l_own belong to head my_head (identical across lane groups
@@ -388,13 +434,15 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[h][e] = 0.0f;
 
-  auto compute_tile = [&](const Tile& tile, auto full_tag) {
-    constexpr bool FULL = decltype(full_tag)::value;
-    float x[4];
+  // Scores of tokens 4g..4g+3 for head my_head, base-2 scaled, -inf where masked.  Branch-free
+  // (the full-tile shortcut is a select) so no control flow sits between the tile's wait and its use.
+  auto qk_phase = [&](const Tile& tile, int slot, float (&x)[4]) {
+    const bool FULL = tile.full;
     if constexpr (QK_MFMA) {
+      const u32x4* src = s_k + slot * KTILE16;
       f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < KSTEPS; ++i) s = E::mfma(tile.k[i], qB[i], s);
+      for (int i = 0; i < KSTEPS; ++i) s = E::mfma(src[kread[i]], qB[i], s);
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] = (FULL || ((tile.valid >> r) & 1u)) ? s[r] * p.scale_log2e : neg_inf;
     } else {
@@ -418,7 +466,10 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
         x[r] = (FULL || ((tile.valid >> r) & 1u)) ? mine * p.scale_log2e : neg_inf;
       }
     }
+  };
 
+  auto pv_phase = [&](const Tile& tile, const float (&x)[4], auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
     // Tile maximum for my_head over the 16 tokens (4 registers x 4 lane groups).
     float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     tmax = max_xor16(tmax);
@@ -481,35 +532,45 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     }
   };
 
-  // Tiles of this wave: t0 = p0 + (wave + kWaves * n) * 16, n < n_tiles.  Register double
-  // buffering with a counted loop: in the steady state every compute is preceded by exactly one
-  // unconditional tile of loads, so the wave waits only for the tile it consumes while the next
-  // one stays in flight (a conditional prefetch makes the memory-counter wait collapse to zero).
-  const int step = kWaves * kTile;
-  const int first = p0 + wave * kTile;
-  const int n_tiles = first < p_end ? (p_end - first + step - 1) / step : 0;
-  auto run_tile = [&](const Tile& tile) {
-    if (tile.full)
-      compute_tile(tile, Flag<true>{});
+  // One tile: wait for `cur`, compute its scores, send out the next tile's loads (if any), then
+  // softmax and PV of `cur` while they are in flight.  Slots and the has-next choice are
+  // compile-time tags so the register tiles stay in registers.
+  //
+  // The wait is explicit: at this point the only memory operations in flight are `cur`'s own (its
+  // K DMA into LDS and its V register loads), so waiting for all of them costs nothing extra, and
+  // it is the wait the LDS reads of the DMA'd K tile need.  The compiler's own counter tracking
+  // does not model LDS-DMA completion precisely; with this unconditional wait ahead of every use
+  // it never has to (and emits no later wait that would also stall on the next tile's loads).
+  auto step = [&](const Tile& cur, auto cur_slot, Tile& next, auto next_slot, int next_t0, auto has_next) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __asm__ __volatile__("" ::: "memory");
+    float x[4];
+    qk_phase(cur, decltype(cur_slot)::value, x);
+    if constexpr (decltype(has_next)::value) issue_tile(next, decltype(next_slot)::value, next_t0);
+    if (cur.full)
+      pv_phase(cur, x, Flag<true>{});
     else
-      compute_tile(tile, Flag<false>{});
+      pv_phase(cur, x, Flag<false>{});
   };
+
+  // Tiles of this wave: t0 = first + n * step_tokens, n < n_tiles.  Two register tiles (and two
+  // LDS K slots) alternate; the loop is peeled so that every load it issues is unconditional.
+  const int step_tokens = kWaves * kTile;
+  const int first = p0 + wave * kTile;
+  const int n_tiles = first < p_end ? (p_end - first + step_tokens - 1) / step_tokens : 0;
   Tile ta, tb;
   if (n_tiles > 0) {
-    load_tile(ta, first);
-    int n = 1;
-    for (; n + 1 < n_tiles; n += 2) {
-      load_tile(tb, first + n * step);
-      run_tile(ta);
-      load_tile(ta, first + (n + 1) * step);
-      run_tile(tb);
+    issue_tile(ta, 0, first);
+    int n = 0;
+    for (; n + 2 < n_tiles; n += 2) {
+      step(ta, Int<0>{}, tb, Int<1>{}, first + (n + 1) * step_tokens, Flag<true>{});
+      step(tb, Int<1>{}, ta, Int<0>{}, first + (n + 2) * step_tokens, Flag<true>{});
     }
-    if (n < n_tiles) {
-      load_tile(tb, first + n * step);
-      run_tile(ta);
-      run_tile(tb);
+    if (n + 1 < n_tiles) {
+      step(ta, Int<0>{}, tb, Int<1>{}, first + (n + 1) * step_tokens, Flag<true>{});
+      step(tb, Int<1>{}, ta, Int<0>{}, 0, Flag<false>{});
     } else {
-      run_tile(ta);
+      step(ta, Int<0>{}, tb, Int<1>{}, 0, Flag<false>{});
     }
   }
 
@@ -523,6 +584,10 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
       float a = sum_xor16(acc[h][e]);
       acc[h][e] = sum_xor32(a);
     }
+  // The staging bytes are reused for the partial accumulators: no DMA may still be writing them
+  // and every wave must be done reading its K slots.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
   if (g == 0) {
 #pragma unroll
     for (int h = 0; h < GC; ++h)

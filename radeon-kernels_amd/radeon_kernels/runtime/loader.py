@@ -109,8 +109,9 @@ class PrecompiledArtifactLoader:
             spec = importlib.util.spec_from_file_location(name, path)
             if spec is None or spec.loader is None:
                 raise ArtifactLoadError(f"cannot create an import specification for {path.name}")
-            module = importlib.util.module_from_spec(spec)
             try:
+                # For a native extension, module_from_spec already dlopens the shared object.
+                module = importlib.util.module_from_spec(spec)
                 spec.loader.exec_module(module)
             except Exception as error:  # import of a shared object can raise anything
                 raise ArtifactLoadError(f"failed to load {path.name}: {error}") from error

@@ -1,0 +1,159 @@
+"""CPU tests of the C ABI (include/rk_paged_attention.h) without launching anything.
+
+* The built library loads and exports every function the header declares.
+* Workspace sizing follows the documented formula.
+* Invalid arguments are rejected with the documented status codes and messages before any launch
+  (every call here fails validation, so no device memory is touched and no GPU is needed).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from radeon_kernels import cabi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "rk_paged_attention.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not cabi.LIBRARY_PATH.is_file():
+        pytest.fail(f"{cabi.LIBRARY_PATH} is not built; run __graft_entry__.build()")
+    return cabi.PagedAttentionLibrary()
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(rk_\w+)\s*\(", text, flags=re.MULTILINE)))
+
+
+def test_header_declares_the_documented_entry_points():
+    assert declared_functions() == sorted(cabi.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib.lib, name), name
+    assert lib.version() == "rk_pa_gfx950 1.0.0 (gfx950, wave64)"
+
+
+def test_status_codes_match_header():
+    text = HEADER.read_text()
+    for name in ("RK_OK", "RK_ERR_INVALID_ARGUMENT", "RK_ERR_UNSUPPORTED", "RK_ERR_WORKSPACE", "RK_ERR_LAUNCH",
+                 "RK_DTYPE_FP16", "RK_DTYPE_BF16", "RK_INDEX_INT32", "RK_INDEX_INT64"):
+        value = int(re.search(rf"#define {name} (\d+)", text).group(1))
+        assert getattr(cabi, name) == value, name
+    assert cabi.VARIANTS == {"mfma": int(re.search(r"RK_PA_VARIANT_MFMA (\d+)", text).group(1)),
+                             "valu": int(re.search(r"RK_PA_VARIANT_VALU (\d+)", text).group(1))}
+
+
+def expected_workspace(batch, hq, d, bs, mb, partition):
+    parts = -(-(mb * bs) // partition)
+    if parts <= 1:
+        return 0
+    records = batch * hq * parts
+    return ((records * d * 4 + 255) // 256) * 256 + records * 2 * 4
+
+
+@pytest.mark.parametrize("shape", [(128, 32, 128, 16, 1024, 2048), (8, 32, 128, 16, 64, 64), (1, 32, 128, 16, 8, 128),
+                                   (4, 16, 64, 32, 64, 128), (3, 12, 256, 1, 700, 256)])
+def test_workspace_size_formula(lib, shape):
+    assert lib.workspace_bytes(*shape) == expected_workspace(*shape)
+
+
+def no_visible_gpu() -> bool:
+    import torch
+
+    return not torch.cuda.is_available()
+
+
+# The calls below pass fake device pointers; each one must fail validation before any launch.  They
+# are skipped where a GPU is visible so that a validation bug could never turn into a launch with
+# invalid pointers.
+cpu_only = pytest.mark.skipif(not no_visible_gpu(), reason="fake-pointer validation checks run without a GPU only")
+
+
+def call(lib, **overrides):
+    args = dict(query=16, key_cache=32, value_cache=48, block_tables=64, context_lengths=80, output=96, workspace=0,
+                workspace_bytes=0, batch=2, query_heads=8, kv_heads=2, head_dim=128, num_blocks=8, block_size=16,
+                max_blocks=4, scale=0.125, dtype=cabi.RK_DTYPE_BF16, index_dtype=cabi.RK_INDEX_INT32,
+                partition_tokens=64, variant=0, stream=0)
+    args.update(overrides)
+    status = lib.decode_raw(**args)
+    return status, lib.last_error()
+
+
+@pytest.mark.parametrize(
+    "overrides, status, message",
+    [
+        (dict(query=0), cabi.RK_ERR_INVALID_ARGUMENT, "must not be NULL"),
+        (dict(dtype=7), cabi.RK_ERR_INVALID_ARGUMENT, "dtype"),
+        (dict(index_dtype=3), cabi.RK_ERR_INVALID_ARGUMENT, "index_dtype"),
+        (dict(variant=9), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        (dict(scale=0.0), cabi.RK_ERR_INVALID_ARGUMENT, "positive and finite"),
+        (dict(scale=float("inf")), cabi.RK_ERR_INVALID_ARGUMENT, "positive and finite"),
+        (dict(query=24), cabi.RK_ERR_UNSUPPORTED, "16-byte aligned"),
+        (dict(head_dim=80), cabi.RK_ERR_INVALID_ARGUMENT, "one of 64, 128, 256"),
+        (dict(query_heads=9), cabi.RK_ERR_INVALID_ARGUMENT, "divisible by kv_heads"),
+        (dict(block_size=48), cabi.RK_ERR_UNSUPPORTED, "power of two"),
+        (dict(block_size=512), cabi.RK_ERR_UNSUPPORTED, "power of two"),
+        (dict(partition_tokens=40), cabi.RK_ERR_INVALID_ARGUMENT, "multiple of 16"),
+        (dict(partition_tokens=8192 * 2), cabi.RK_ERR_INVALID_ARGUMENT, "multiple of 16"),
+        (dict(partition_tokens=8192, block_size=16), cabi.RK_ERR_INVALID_ARGUMENT, "<= 256"),
+        (dict(batch=0), cabi.RK_ERR_INVALID_ARGUMENT, "positive"),
+        (dict(num_blocks=1 << 31), cabi.RK_ERR_UNSUPPORTED, "32-bit"),
+        (dict(kv_heads=1 << 19, query_heads=1 << 19), cabi.RK_ERR_UNSUPPORTED, "too large"),
+        (dict(max_blocks=64, partition_tokens=64), cabi.RK_ERR_WORKSPACE, "workspace of"),
+        (dict(max_blocks=64, partition_tokens=64, workspace=4096 + 64, workspace_bytes=1 << 20), cabi.RK_ERR_WORKSPACE,
+         "256-byte aligned"),
+    ],
+)
+@cpu_only
+def test_invalid_arguments_are_rejected_before_launch(lib, overrides, status, message):
+    got, text = call(lib, **overrides)
+    assert got == status, text
+    assert message in text
+
+
+@cpu_only
+def test_phase_entry_points_validate_identically(lib):
+    for phase in ("partitions", "reduce"):
+        status = lib.decode_raw(query=0, key_cache=32, value_cache=48, block_tables=64, context_lengths=80, output=96,
+                                workspace=0, workspace_bytes=0, batch=2, query_heads=8, kv_heads=2, head_dim=128,
+                                num_blocks=8, block_size=16, max_blocks=4, scale=0.125, dtype=1, index_dtype=0,
+                                partition_tokens=64, variant=0, stream=0, phase=phase)
+        assert status == cabi.RK_ERR_INVALID_ARGUMENT and "NULL" in lib.last_error()
+
+
+@cpu_only
+def test_last_error_is_per_thread(lib):
+    import threading
+
+    call(lib, dtype=7)
+    seen = {}
+
+    def worker():
+        call(lib, variant=9)
+        seen["thread"] = lib.last_error()
+
+    thread = threading.Thread(target=worker)
+    thread.start()
+    thread.join()
+    assert "variant" in seen["thread"]
+    assert "dtype" in lib.last_error()
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(FileNotFoundError, match="build"):
+        cabi.PagedAttentionLibrary(tmp_path / "absent.so")
+
+
+def test_workspace_null_pointer_rejected(lib):
+    out = ctypes.c_size_t(0)
+    assert lib.lib.rk_pa_decode_workspace_bytes(1, 8, 128, 16, 4, 64, None) == cabi.RK_ERR_INVALID_ARGUMENT
+    assert lib.lib.rk_pa_decode_workspace_bytes(1, 8, 128, 16, 4, 64, ctypes.byref(out)) == cabi.RK_OK

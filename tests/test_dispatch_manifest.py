@@ -1,0 +1,149 @@
+"""The shipped gfx950 dispatch manifest and kernel pack.
+
+* The manifest parses strictly and every measured workload's signature (built by the public API's
+  own signature code) selects its exact gfx950 entry; other gfx950 shapes select the broad region;
+  shapes the kernel does not handle select nothing (declared torch fallback).
+* The gfx950 entries merge into the reference's published paged-attention manifest (a committed
+  data fixture) and the merged document still validates: different architectures never overlap.
+* The pack manifest and the dispatch winners agree on artifact, digest and environment, and the
+  digest is the built binding's.
+"""
+
+from __future__ import annotations
+
+import copy
+import hashlib
+import json
+from pathlib import Path
+
+import pytest
+
+from radeon_kernels import dispatch_plan
+from radeon_kernels.ops.paged_attention.api import _execute
+from radeon_kernels.runtime.dispatcher import DispatchRequest, Dispatcher
+from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint
+from radeon_kernels.runtime.pack import KernelPack
+from radeon_kernels.runtime.registry import DispatchManifest, DispatchRegistry
+from radeon_kernels.runtime.resources import builtin_contract, builtin_dispatch_registry
+from radeon_kernels.workloads import WORKLOADS
+from test_api import CaptureRuntime, FakeTensor, FakeTorch
+
+ROOT = Path(__file__).resolve().parents[1]
+PACK = ROOT / "radeon-kernels_amd" / "packs" / "gfx950"
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def gfx950_manifest() -> DispatchManifest:
+    return builtin_dispatch_registry().get("paged_attention_decode", "1.0")
+
+
+def gfx950_fingerprint() -> EnvironmentFingerprint:
+    env = gfx950_manifest().entries[0].environment
+    return EnvironmentFingerprint(architecture=env.architecture, wavefront_size=env.wavefront_size,
+                                  rocm_abi=env.rocm_abi, python_abi=env.python_abi,
+                                  pytorch_version=env.pytorch_version)
+
+
+def signature_for(batch, hq, hkv, d, num_blocks, bs, mb, dtype="bf16", index="int32", scale=None):
+    torch_dtype = {"fp16": "float16", "bf16": "bfloat16"}[dtype]
+    runtime = CaptureRuntime()
+    _execute(FakeTensor((batch, hq, d), dtype=torch_dtype), FakeTensor((num_blocks, bs, hkv, d), dtype=torch_dtype),
+             FakeTensor((num_blocks, bs, hkv, d), dtype=torch_dtype), FakeTensor((batch, mb), dtype=index),
+             FakeTensor((batch,), dtype=index), scale, torch_module=FakeTorch(), runtime=runtime)
+    return runtime.call["signature"]
+
+
+def select(signature):
+    return Dispatcher(builtin_dispatch_registry()).select(
+        DispatchRequest("paged_attention_decode", "1.0", signature), gfx950_fingerprint())
+
+
+def test_manifest_is_gfx950_only_wave64_and_strict():
+    manifest = gfx950_manifest()
+    assert len(manifest.entries) == len(dispatch_plan.EXACT_REGIONS) + 1
+    for entry in manifest.entries:
+        assert entry.environment.architecture == "gfx950" and entry.environment.wavefront_size == 64
+        assert entry.winner.provider == "native" and entry.winner.format == "python_extension"
+        assert entry.fallbacks == ("torch",)
+    assert manifest.default_fallbacks == ("torch",)
+
+
+EXPECTED = {
+    "c1": ("paged_attention_decode-gfx950-b1-gqa32x8-c128-d128-p16-fp16", 64, 8),
+    "c2": ("paged_attention_decode-gfx950-b8-gqa32x8-c1024-d128-p16-bf16", 1024, 64),
+    "c3": ("paged_attention_decode-gfx950-b4-mha16-c2048-d64-p32-bf16", 512, 64),
+    "c4": ("paged_attention_decode-gfx950-b4-gqa32x8-c1024-d256-p16-fp16", 512, 64),
+    "c5": ("paged_attention_decode-gfx950-b128-gqa32x8-ragged-d128-p16-bf16", 69713, 1024),
+}
+
+
+@pytest.mark.parametrize("key", sorted(EXPECTED))
+@pytest.mark.parametrize("index", ["int32", "int64"])
+@pytest.mark.parametrize("scale", [None, 0.1])
+def test_measured_workloads_select_their_exact_entry(key, index, scale):
+    w = WORKLOADS[key]
+    entry_id, num_blocks, mb = EXPECTED[key]
+    signature = signature_for(w.batch, w.query_heads, w.kv_heads, w.head_dim, num_blocks, w.block_size, mb,
+                              w.dtype, index, scale)
+    decision = select(signature)
+    assert decision.entry_id == entry_id
+    assert decision.winner.entrypoint == "decode_mfma"
+    assert decision.launch["partition_tokens"] >= 16
+
+
+def test_other_gfx950_shapes_use_broad_region_and_unsupported_ones_fall_back():
+    broad = select(signature_for(3, 12, 4, 128, 99, 32, 40, "fp16", "int64"))
+    assert broad.entry_id == "paged_attention_decode-gfx950-region"
+    assert dict(broad.launch) == dispatch_plan.BROAD_LAUNCH
+    none = select(signature_for(2, 8, 2, 64, 8, 48, 4))  # block size 48 is not a power of two
+    assert not none.matched and none.fallbacks == ("torch",)
+
+
+def test_entries_merge_into_the_reference_manifest():
+    reference = json.loads((GOLDEN / "reference_dispatch_paged_attention_decode-1.0.json").read_text())
+    reference_manifest = DispatchManifest.from_mapping(reference, "reference")
+    assert len(reference_manifest.entries) == 25
+    ours = json.loads((ROOT / "radeon-kernels_amd" / "radeon_kernels" / "dispatch"
+                       / "paged_attention_decode-1.0.json").read_text())
+    merged = copy.deepcopy(reference)
+    merged["entries"].extend(ours["entries"])
+    parsed = DispatchManifest.from_mapping(merged, "merged")
+    assert len(parsed.entries) == 25 + len(ours["entries"])
+    # The published entries still select exactly as before on their own architectures.
+    for entry in reference_manifest.entries:
+        fp = EnvironmentFingerprint(architecture=entry.environment.architecture,
+                                    wavefront_size=entry.environment.wavefront_size,
+                                    rocm_abi=entry.environment.rocm_abi, python_abi=entry.environment.python_abi,
+                                    pytorch_version=entry.environment.pytorch_version)
+        signature = {key: constraint.value for key, constraint in entry.workload.values.items()}
+        decision = Dispatcher(DispatchRegistry([parsed])).select(
+            DispatchRequest("paged_attention_decode", "1.0", signature), fp)
+        assert decision.entry_id == entry.id
+
+
+def test_pack_manifest_agrees_with_dispatch_and_binary():
+    pack = KernelPack.from_directory(PACK, verify_artifacts=False)
+    manifest = gfx950_manifest()
+    item = pack.get("paged_attention_decode", "1.0")
+    for entry in manifest.entries:
+        assert entry.winner == item.artifact
+        assert entry.evidence_id == item.evidence_id
+        assert entry.environment == pack.environment
+    binary = PACK / item.artifact.artifact
+    if binary.is_file():  # built by build(); not part of the source tree
+        assert hashlib.sha256(binary.read_bytes()).hexdigest() == item.artifact.sha256
+        KernelPack.from_directory(PACK, verify_artifacts=True)
+
+
+def test_contract_document_matches_the_api():
+    contract = builtin_contract("paged_attention_decode", "1.0")
+    assert contract["parameters"]["cache_layout"] == "block_slot_head_dim"
+    assert contract["parameters"]["query_to_kv_head"] == "query_head//(query_heads//kv_heads)"
+    assert contract["capabilities"] == {"inference": True, "backward": False, "deterministic": True,
+                                        "graph_capture": True}
+    assert contract["reference"]["entrypoint"] == (
+        "radeon_kernels.ops.paged_attention.reference.paged_attention_decode_reference")
+    import importlib
+
+    module_name, _, function = contract["reference"]["entrypoint"].rpartition(".")
+    assert callable(getattr(importlib.import_module(module_name), function))

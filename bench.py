@@ -223,6 +223,26 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         hot = round((time.perf_counter() - t) / args.steps * 1e6, 2)
 
+    # The public operator end to end (validation, dispatch, pack lookup, output and workspace
+    # allocation, both launches) on the same inputs, back to back.
+    import warnings
+
+    import radeon_kernels as rk
+    from radeon_kernels.ops._runtime import NativeDemotionWarning
+
+    k, v = caches[0]
+    with warnings.catch_warnings():
+        # A demotion would run the torch fallback (tens of GB of intermediates at this size).
+        warnings.simplefilter("error", NativeDemotionWarning)
+        rk.paged_attention_decode(q, k, v, bt, cl)
+    decision = rk.get_last_dispatch()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        rk.paged_attention_decode(q, k, v, bt, cl)
+    torch.cuda.synchronize()
+    rk_us = (time.perf_counter() - t) / args.steps * 1e6
+
     traffic = read_traffic(w.name, variant, partition)
     result = {
         "metric": METRIC,
@@ -249,7 +269,8 @@ def main(argv=None) -> int:
         "pct_hbm_peak": round(gbps / HBM_PEAK_GBPS * 100, 2),
         "kv_bytes_per_call": kv_bytes,
         "kernels_us": {
-            "pa_partition_kernel": {"avg": round(part_avg, 2), "min": round(min(part_us), 2), "max": round(max(part_us), 2)},
+            "pa_partition_kernel": {"avg": round(part_avg, 2), "min": round(min(part_us), 2), "max": round(max(part_us), 2),
+                                    "cv": round(statistics.pstdev(part_us) / part_avg, 4)},
             "pa_reduce_kernel": {"avg": round(statistics.fmean(red_us), 2), "min": round(min(red_us), 2),
                                  "max": round(max(red_us), 2)},
         },
@@ -264,6 +285,8 @@ def main(argv=None) -> int:
     }
     if hot is not None:
         result["us_per_call_cache_resident"] = hot
+    result["rk_call"] = {"us_per_call": round(rk_us, 2), "selected": decision["selected"],
+                         "entry_id": decision["entry_id"], "cache_resident": copies > 1}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, data, args.cpu_seconds)
     else:

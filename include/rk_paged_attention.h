@@ -75,8 +75,8 @@ int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t hea
 /*
  * Paged-attention decode: one query token per sequence against the paged K/V cache.
  *
- * partition_tokens: context tokens per workgroup (split-K partition); a multiple of 64 in
- *   [64, 8192] with partition_tokens / block_size <= 256.
+ * partition_tokens: context tokens per workgroup (split-K partition); a multiple of 16 in
+ *   [16, 8192] with partition_tokens / block_size <= 256.
  * variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_VALU.
  * workspace/workspace_bytes: device buffer of at least rk_pa_decode_workspace_bytes(...) bytes
  *   (may be NULL/0 when that is zero).  Its contents need no initialisation.

@@ -11,7 +11,8 @@
 //
 //   pa_partition_kernel  one 256-thread workgroup per (sequence, KV head, head chunk, context
 //                        partition).  Each of its 4 waves walks 16-token tiles of the partition.
-//                        K rows are fetched as 16-byte lane loads straight into MFMA A operands
+//                        K rows are copied by global_load_lds DMA into a double-buffered,
+//                        XOR-swizzled per-wave LDS tile and read from there as MFMA A operands
 //                        (tokens on M, query heads of the chunk replicated over N); V rows are
 //                        fetched as full-row lane-group loads (one token row per 16 lanes) and
 //                        consumed by fp32 FMAs.  The 16x16 MFMA accumulator layout puts the score

@@ -54,7 +54,7 @@ class NativeDemotionWarning(RuntimeWarning):
 def _record(decision: DispatchDecision, *, selected: str, artifact: str | None, evidence_id: str | None, reason: str) -> None:
     record = decision.to_dict()
     record.update(selected=selected, artifact=artifact, evidence_id=evidence_id, reason=reason)
-    record_dispatch(record)
+    record_dispatch(record, owned=True)
 
 
 class OperatorRuntime:
@@ -110,7 +110,8 @@ class OperatorRuntime:
         fallback_selected: str,
     ) -> Any:
         fingerprint = self.fingerprint(torch_module, device_index)
-        decision = self._dispatcher.select(DispatchRequest(operator, semantic_version, signature), fingerprint)
+        decision = self._dispatcher.select(DispatchRequest(operator, semantic_version, signature), fingerprint,
+                                           record=False)
         failure: str | None = None
         if decision.matched:
             winner = decision.winner

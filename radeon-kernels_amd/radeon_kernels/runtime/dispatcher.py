@@ -1,8 +1,12 @@
 """Static dispatch: pick the highest-priority manifest entry matching (environment, signature).
 
 Interface of src/radeon_kernels/runtime/dispatcher.py:11-100 in the reference.  Every selection,
-matched or not, is written to the explain record.  No search, tuning or compilation happens here:
-an unmatched request gets the manifest's declared fallbacks.
+matched or not, is written to the explain record (the operator runtime, which records the final
+outcome of each call itself, asks for no intermediate record).  No search, tuning or compilation
+happens here: an unmatched request gets the manifest's declared fallbacks.
+
+Manifests are immutable once loaded, so a decision depends only on (operator, version, fingerprint,
+signature); decisions are memoised on that key (the reference rescans every entry per call).
 """
 
 from __future__ import annotations
@@ -58,10 +62,30 @@ class DispatchDecision:
 
 
 class Dispatcher:
+    _CACHE_LIMIT = 4096
+
     def __init__(self, registry: DispatchRegistry) -> None:
         self._registry = registry
+        self._decisions: dict[Any, DispatchDecision] = {}
 
-    def select(self, request: DispatchRequest, fingerprint: EnvironmentFingerprint) -> DispatchDecision:
+    def select(self, request: DispatchRequest, fingerprint: EnvironmentFingerprint, *,
+               record: bool = True) -> DispatchDecision:
+        try:
+            key = (request.operator, request.semantic_version, fingerprint, tuple(request.signature.items()))
+            decision = self._decisions.get(key)
+        except TypeError:  # an unhashable signature value: decide without memoising
+            key, decision = None, None
+        if decision is None:
+            decision = self._decide(request, fingerprint)
+            if key is not None:
+                if len(self._decisions) >= self._CACHE_LIMIT:
+                    self._decisions.clear()
+                self._decisions[key] = decision
+        if record:
+            record_dispatch(decision.to_dict(), owned=True)
+        return decision
+
+    def _decide(self, request: DispatchRequest, fingerprint: EnvironmentFingerprint) -> DispatchDecision:
         manifest = self._registry.get(request.operator, request.semantic_version)
         best = None
         for entry in manifest.entries:
@@ -94,5 +118,4 @@ class Dispatcher:
                 evidence_id=best.evidence_id,
                 reason=f"matched dispatch entry {best.id!r} at priority {best.priority}",
             )
-        record_dispatch(decision.to_dict())
         return decision

@@ -3,7 +3,9 @@
 Interface of src/radeon_kernels/runtime/explain.py:8-46 in the reference: the record lives in a
 ContextVar (one per thread / async task) and ``explain_last_dispatch()`` renders seven lines --
 operator, architecture, selected, artifact, evidence, fallbacks (joined by " -> ") and reason.
-Records are copied on the way in and out, so callers cannot mutate the stored decision.
+Records are copied on the way in and out, so callers cannot mutate the stored decision (a caller
+that builds a fresh record for the purpose hands it over with ``owned=True`` and skips the inbound
+copy; the reference deep-copies twice per dispatch).
 """
 
 from __future__ import annotations
@@ -15,8 +17,14 @@ from typing import Any, Mapping
 _LAST: ContextVar[dict[str, Any] | None] = ContextVar("radeon_kernels_last_dispatch", default=None)
 
 
-def record_dispatch(value: Mapping[str, Any]) -> None:
-    _LAST.set(deepcopy(dict(value)))
+def record_dispatch(value: Mapping[str, Any], *, owned: bool = False) -> None:
+    """Store ``value`` as this context's last decision.
+
+    ``owned=True`` promises that ``value`` is a dict built for this call whose nested containers
+    nobody else holds, so it is stored without a copy.
+    """
+
+    _LAST.set(value if owned and type(value) is dict else deepcopy(dict(value)))
 
 
 def get_last_dispatch() -> dict[str, Any] | None:

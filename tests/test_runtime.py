@@ -234,6 +234,38 @@ def test_returns_declared_fallback_without_search(dispatcher):
     assert not other.matched
 
 
+def test_decisions_are_memoised_and_still_recorded(dispatcher):
+    first = dispatcher.select(request(128), fingerprint())
+    clear_last_dispatch()
+    again = dispatcher.select(request(128), fingerprint())
+    assert again is first  # same (operator, version, fingerprint, signature) -> the same decision
+    assert get_last_dispatch()["entry_id"] == "exact"  # every select still writes the record
+    assert dispatcher.select(request(64), fingerprint()).entry_id == "broad"  # other keys decide afresh
+    assert dispatcher.select(request(128), fingerprint(architecture="gfx942")).matched is False
+    clear_last_dispatch()
+    assert dispatcher.select(request(128), fingerprint(), record=False) is first
+    assert get_last_dispatch() is None
+    # An unhashable signature value (keys no entry constrains are ignored by matching) is decided
+    # without memoising, with the same result.
+    odd = DispatchRequest("paged_attention_decode", "1.0", {"dtype": "bf16", "batch": 128, "head_dim": 128,
+                                                            "extra": ["unhashable"]})
+    decided = dispatcher.select(odd, fingerprint())
+    assert decided.entry_id == "exact" and decided is not first
+
+
+def test_owned_records_skip_the_inbound_copy_but_reads_still_copy():
+    clear_last_dispatch()
+    value = {"operator": "x", "architecture": "gfx950", "reason": "r", "launch": {"partition_tokens": 64}}
+    record_dispatch(value, owned=True)
+    out = get_last_dispatch()
+    out["launch"]["partition_tokens"] = 1
+    assert get_last_dispatch()["launch"] == {"partition_tokens": 64}
+    shared = {"operator": "x", "architecture": "gfx950", "reason": "r", "launch": {"partition_tokens": 64}}
+    record_dispatch(shared)  # not owned: copied on the way in
+    shared["launch"]["partition_tokens"] = 2
+    assert get_last_dispatch()["launch"] == {"partition_tokens": 64}
+
+
 def test_explain_text_and_isolation():
     clear_last_dispatch()
     assert explain_last_dispatch() == "No Radeon kernel dispatch has been performed in this context."

@@ -146,11 +146,18 @@ def compile_libraries(verbose: bool = False) -> tuple[Path, Path]:
     ]
     gxx = _run(cxx, verbose)
     _finish(hip, "hipcc (C-ABI library)")
+    # The binding checks at import that the kernel library it loads is the one built here.
+    digest_src = work / "kernel_digest.cpp"
+    digest_obj = work / "kernel_digest.o"
+    digest_src.write_text(f'extern const char kRkKernelLibrarySha256[] = "{sha256_file(cabi_tmp)}";\n')
+    _finish(_run(["g++", "-O2", "-fPIC", "-c", str(digest_src), "-o", str(digest_obj)], verbose),
+            "g++ (kernel library digest)")
     _finish(gxx, "g++ (torch binding)")
     link = [
         "g++",
         "-shared",
         str(ext_obj),
+        str(digest_obj),
         f"-L{work}",
         *[f"-L{path}" for path in libraries],
         "-l:" + CABI_NAME,
@@ -169,6 +176,7 @@ def compile_libraries(verbose: bool = False) -> tuple[Path, Path]:
     os.replace(cabi_tmp, LIB_DIR / CABI_NAME)
     os.replace(ext_tmp, LIB_DIR / f"{EXTENSION_NAME}.so")
     ext_obj.unlink()
+    digest_obj.unlink()
     return LIB_DIR / CABI_NAME, LIB_DIR / f"{EXTENSION_NAME}.so"
 
 

@@ -147,3 +147,40 @@ def test_contract_document_matches_the_api():
 
     module_name, _, function = contract["reference"]["entrypoint"].rpartition(".")
     assert callable(getattr(importlib.import_module(module_name), function))
+
+
+def _binding_import_script(lib_dir: Path) -> str:
+    return (
+        "import sys, importlib.util\n"
+        "import torch\n"
+        f"spec = importlib.util.spec_from_file_location('rk_pa_gfx950', r'{lib_dir / 'rk_pa_gfx950.so'}')\n"
+        "module = importlib.util.module_from_spec(spec)\n"
+        "spec.loader.exec_module(module)\n"
+        "print(module.kernel_library_sha256)\n"
+    )
+
+
+def test_binding_pins_the_kernel_library_it_loads(tmp_path):
+    """The pack digest names the binding; the binding refuses a kernel library other than its own."""
+
+    import shutil
+    import subprocess
+    import sys
+
+    lib_dir = PACK / "lib"
+    if not (lib_dir / "rk_pa_gfx950.so").is_file():
+        pytest.fail("the kernel pack is not built; run __graft_entry__.build()")
+    expected = hashlib.sha256((lib_dir / "librk_pa_gfx950.so").read_bytes()).hexdigest()
+    ok = subprocess.run([sys.executable, "-c", _binding_import_script(lib_dir)], capture_output=True, text=True,
+                        timeout=300)
+    assert ok.returncode == 0, ok.stderr
+    assert ok.stdout.strip().splitlines()[-1] == expected
+    # A copy of the pack whose kernel library differs by one appended byte must not import.
+    copy = tmp_path / "lib"
+    shutil.copytree(lib_dir, copy)
+    with (copy / "librk_pa_gfx950.so").open("ab") as stream:
+        stream.write(b"\0")
+    bad = subprocess.run([sys.executable, "-c", _binding_import_script(copy)], capture_output=True, text=True,
+                         timeout=300)
+    assert bad.returncode != 0
+    assert "this module was built against" in bad.stderr

@@ -11,7 +11,7 @@
 //
 //   pa_partition_kernel  one 256-thread workgroup per (sequence, KV head, head chunk, context
 //                        partition).  Each of its 4 waves walks 16-token tiles of the partition.
-//                        K rows are copied by global_load_lds DMA into a double-buffered,
+//                        K rows are copied by global_load_lds DMA into a multi-buffered,
 //                        XOR-swizzled per-wave LDS tile and read from there as MFMA A operands
 //                        (tokens on M, query heads of the chunk replicated over N); V rows are
 //                        fetched as full-row lane-group loads (one token row per 16 lanes) and
@@ -46,11 +46,17 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kTile = 16;             // tokens per wave step = MFMA M
+constexpr int kXcds = 8;              // accelerator complex dies; workgroup h runs on XCD h % 8
+constexpr int64_t kXcdGroupedItems = 4096;
 constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, plus one straddle
 constexpr float kLog2e = 1.4426950408889634f;
-// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 only: vmcnt bits [3:0] and [15:14]
-// zero, expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait on those counters).
-constexpr int kWaitVmcnt0 = 0x0F70;
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory operations are
+// outstanding: vmcnt in bits [3:0] and [15:14], expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait on
+// those counters).  Vector memory loads, LDS DMA included, retire in issue order, so vmcnt <= n
+// means everything but the n most recently issued operations has landed.
+constexpr int wait_vmcnt(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
+// ... and the one that waits for lgkmcnt == 0 only (LDS and scalar memory), vmcnt left at its maximum.
+constexpr int kWaitLgkmcnt0 = 0xC07F;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -144,6 +150,56 @@ __device__ __forceinline__ void dma_to_lds16(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
 }
 
+// LDS reads that complete before they return (ds_read + s_waitcnt lgkmcnt(0) in one statement).
+// The compiler places a conservative vmcnt(0) wait in front of every LDS read it emits while an
+// LDS-DMA is outstanding, since it cannot tell which LDS bytes the DMA writes; that wait would stall
+// on the loads of tiles still in flight.  The kernel issues these reads only after its own explicit
+// memory-counter wait has covered the DMA that wrote the bytes being read.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  typedef const __attribute__((address_space(3))) char lds_char;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)(p)));
+}
+
+__device__ __forceinline__ int lds_read_i32_sync(uint32_t addr) {
+  int v;
+  __asm__ __volatile__("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+template <int OFFSET>
+__device__ __forceinline__ void lds_read2x16_sync(u32x4& a, u32x4& b, uint32_t aa, uint32_t ab) {
+  __asm__ __volatile__(
+      "ds_read_b128 %0, %2 offset:%4\n\t"
+      "ds_read_b128 %1, %3 offset:%4\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a), "=&v"(b)
+      : "v"(aa), "v"(ab), "i"(OFFSET)
+      : "memory");
+}
+
+template <int OFFSET>
+__device__ __forceinline__ void lds_read4x16_sync(u32x4& a, u32x4& b, u32x4& c, u32x4& d, uint32_t aa,
+                                                  uint32_t ab, uint32_t ac, uint32_t ad) {
+  __asm__ __volatile__(
+      "ds_read_b128 %0, %4 offset:%8\n\t"
+      "ds_read_b128 %1, %5 offset:%8\n\t"
+      "ds_read_b128 %2, %6 offset:%8\n\t"
+      "ds_read_b128 %3, %7 offset:%8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
+      : "v"(aa), "v"(ab), "v"(ac), "v"(ad), "i"(OFFSET)
+      : "memory");
+}
+
+// Workgroup barrier that publishes this wave's LDS writes but, unlike __syncthreads, does not wait
+// for its outstanding global loads (the K/V loads already in flight stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
+
 template <bool B>
 struct Flag {
   static constexpr bool value = B;
@@ -157,6 +213,22 @@ struct Int {
 __device__ __forceinline__ int64_t load_index(const void* base, int64_t i, bool is64) {
   return is64 ? static_cast<const int64_t*>(base)[i]
               : static_cast<int64_t>(static_cast<const int32_t*>(base)[i]);
+}
+
+// The two 32-bit words of an index element, loaded without branching on the index type (for int32
+// both words are the element itself); decoded by index_value once the loads have landed.  Keeps
+// independent index loads in flight together instead of waiting on each at an int32/int64 merge.
+struct RawIndex {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ RawIndex load_raw_index(const void* base, int64_t i, bool is64) {
+  const uint32_t* words = static_cast<const uint32_t*>(base);
+  const int64_t at = is64 ? 2 * i : i;
+  return RawIndex{words[at], words[is64 ? at + 1 : at]};
+}
+__device__ __forceinline__ int64_t index_value(RawIndex r, bool is64) {
+  return is64 ? static_cast<int64_t>((static_cast<uint64_t>(r.hi) << 32) | r.lo)
+              : static_cast<int64_t>(static_cast<int32_t>(r.lo));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -181,6 +253,7 @@ struct Params {
   int32_t bs_log2;
   int32_t partition_tokens;
   int32_t num_partitions;  // ceil(max_blocks * BS / partition_tokens)
+  int32_t xcd_grouped;     // 1: head slots of a work item share an XCD (grid padded to whole rounds)
   int32_t index_is64;
   float scale_log2e;
 };
@@ -201,12 +274,14 @@ __device__ __forceinline__ int64_t clamped_context(const Params& p, int b) {
 //           wave-uniform and addresses are a scalar base plus fixed 32-bit per-lane offsets
 //
 // MFMA variant data path per 16-token tile and wave:
-//   K: global_load_lds_dwordx4 straight into a per-wave LDS slot (two slots, double buffered).
-//      Each DMA instruction moves whole cache rows (coalesced); lane l fetches chunk
-//      (l % CPR) ^ (row & SWZ) of its row, so the hardware's lane-contiguous LDS write leaves the
-//      tile XOR-swizzled and the MFMA operand read (token j, chunk 4i+g) is bank-conflict free.
+//   K: global_load_lds_dwordx4 straight into a per-wave LDS slot.  Each DMA instruction moves
+//      whole cache rows (coalesced); lane l fetches chunk (l % CPR) ^ (row & SWZ) of its row, so
+//      the hardware's lane-contiguous LDS write leaves the tile XOR-swizzled and the MFMA operand
+//      read (token j, chunk 4i+g) is bank-conflict free.
 //   V: 16-byte register loads, one token row per 16-lane group (rows 4g..4g+3).
-//   Order: read K(n) from LDS -> MFMA -> issue K(n+1) DMA and V(n+1) loads -> softmax -> PV(n).
+//   Pipeline: DEPTH tiles are in flight ahead of the one being computed (DEPTH + 1 register tiles
+//   and LDS K slots rotate).  Step n: wait until tile n has landed -> issue tile n + DEPTH ->
+//   read K(n) from LDS -> MFMA -> softmax -> PV(n).
 template <class E, int D, int GC, bool QK_MFMA, bool UB>
 __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   constexpr int KSTEPS = D / 32;       // MFMA k-steps; also DMA instructions per K tile
@@ -219,10 +294,21 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   static_assert(GC == 1 || GC == 2 || GC == 4, "head chunk must be 1, 2 or 4");
   static_assert(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
   static_assert(KTILE16 == KSTEPS * kWave, "one DMA instruction per MFMA k-step");
+  // Tiles in flight ahead of the current one: two when K is staged in LDS, blocks hold whole tiles
+  // and head_dim <= 128; one for head_dim 256 (K slots twice as large, register file already mostly
+  // used), for the VALU variant (K rows held in registers: a third tile would push it to one wave
+  // per SIMD) and for blocks smaller than a tile (per-lane block-table reads in LDS).
+  constexpr int DEPTH = (QK_MFMA && UB && D != 256) ? 2 : 1;
+  constexpr int SLOTS = DEPTH + 1;
+  // Vector memory instructions one tile issues (K DMA or K rows, then V rows): the unit of the
+  // explicit memory-counter waits.
+  constexpr int ROW_LOADS = 4 * (VW >= 4 ? VW / 4 : 1);
+  constexpr int TILE_OPS = (QK_MFMA ? KSTEPS : ROW_LOADS) + ROW_LOADS;
 
   // The K staging slots and, after the main loop, the per-wave partial accumulators share one
   // LDS buffer (a barrier separates the two uses).
-  constexpr int K_STAGE_BYTES = QK_MFMA ? kWaves * 2 * KTILE16 * 16 : 0;
+  constexpr int SLOT_BYTES = KTILE16 * 16;
+  constexpr int K_STAGE_BYTES = QK_MFMA ? kWaves * SLOTS * SLOT_BYTES : 0;
   constexpr int ACC_BYTES = kWaves * GC * D * 4;
   constexpr int RAW_BYTES = K_STAGE_BYTES > ACC_BYTES ? K_STAGE_BYTES : ACC_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char s_raw[RAW_BYTES];
@@ -235,16 +321,29 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   const int lane = tid & 63;
   const int g = lane >> 4;   // lane group: owns tokens 4g..4g+3 of every tile (V / scores)
   const int j = lane & 15;   // lane in group: token j of the tile for K (MFMA), V column block
-  u32x4* const s_k = reinterpret_cast<u32x4*>(s_raw) + wave * 2 * KTILE16;
+  u32x4* const s_k = reinterpret_cast<u32x4*>(s_raw) + wave * SLOTS * KTILE16;
   float(*const s_acc)[GC][D] = reinterpret_cast<float(*)[GC][D]>(s_raw);
 
-  // Workgroup -> (partition, sequence, KV head, head chunk), KV head / chunk varying fastest and
-  // partition slowest.  The workgroups of all KV heads of one token range are dispatched together,
-  // so the cache rows of a token (its KV heads are adjacent in memory) are requested close
-  // together in time, which keeps DRAM row-buffer locality (measured +13% over a partition-fastest
-  // order on the 128-sequence ragged workload); partition-major order then lets the early-exiting
-  // workgroups of short sequences cluster at the end of the grid.
-  const int64_t wg = blockIdx.x;
+  // Workgroup -> (partition, sequence, KV head, head chunk).  Work items are ordered head slot
+  // (KV head, head chunk) fastest, then sequence, then partition, and the hardware id is mapped so
+  // that all head slots of one (sequence, partition) run on the same XCD while successive
+  // (sequence, partition) items go round-robin over the 8 XCDs (the dispatcher places hardware
+  // workgroup h on XCD h % 8).  The cache rows of a token are adjacent in memory across KV heads,
+  // so one XCD then requests each token's rows together (measured +2% over spreading the head slots
+  // over XCDs, +13% for partition-slowest over partition-fastest on the 128-sequence ragged
+  // workload); partition-major order lets the early-exiting workgroups of short sequences cluster
+  // at the end of the grid.  The host pads the grid to a multiple of 8 * head slots; padding
+  // workgroups (item index past the end) exit at once.  Grids of fewer than kXcdGroupedItems items
+  // (one or two rounds of workgroups, latency-bound) keep the identity mapping, which measured
+  // about 0.5 us faster there.
+  const int64_t heads_per_seq64 = static_cast<int64_t>(p.kv_heads) * p.head_chunks;
+  const int64_t hw = blockIdx.x;
+  int64_t wg = hw;
+  if (p.xcd_grouped) {
+    const int64_t hw_row = hw / kXcds;
+    wg = ((hw_row / heads_per_seq64) * kXcds + hw % kXcds) * heads_per_seq64 + hw_row % heads_per_seq64;
+    if (wg >= heads_per_seq64 * p.batch * p.num_partitions) return;
+  }
   const int heads_per_seq = p.kv_heads * p.head_chunks;
   const int hslot = static_cast<int>(wg % heads_per_seq);
   const int64_t rest = wg / heads_per_seq;
@@ -255,34 +354,26 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   const int head0 = kvh * p.group + chunk * GC;  // first query head of this chunk
   const int heads_here = min(GC, p.group - chunk * GC);
 
-  const int64_t ctx = clamped_context(p, b);
-  if (ctx <= 0) {
-    // Softmax over an empty set: NaN, as the fallback produces.  Partition 0 owns the output.
-    if (part == 0) {
-      for (int idx = tid; idx < heads_here * D; idx += kThreads) {
-        const int h = idx / D, d = idx % D;
-        p.out[(static_cast<int64_t>(b) * p.query_heads + head0 + h) * D + d] =
-            E::store(__builtin_nanf(""));
-      }
-    }
-    return;
-  }
+  // Prologue.  Every load that does not depend on the context length -- the context length
+  // itself, this partition's block-table slice, the query and (uniform-block path) the block ids of
+  // the wave's first tiles -- is issued together, so the workgroup waits one memory latency, not
+  // three, before it sends out its first K/V loads.
   const int P = p.partition_tokens;
-  const int np = static_cast<int>((ctx + P - 1) / P);
-  if (part >= np) return;
-  const int p0 = part * P;
-  const int p_end = static_cast<int>(min(static_cast<int64_t>(p0 + P), ctx));
   const int lb = p.bs_log2;
   const int bs_mask = (1 << lb) - 1;
-
-  // Stage this partition's block-table slice in LDS (-1 marks ids outside [0, num_blocks)).
+  const int p0 = part * P;
   const int blk0 = p0 >> lb;
-  const int nblk = ((p_end - 1) >> lb) - blk0 + 1;
-  for (int i = tid; i < nblk; i += kThreads) {
-    const int64_t id = load_index(p.block_tables,
-                                  static_cast<int64_t>(b) * p.max_blocks + blk0 + i,
-                                  p.index_is64 != 0);
-    s_table[i] = (id >= 0 && id < p.num_blocks) ? static_cast<int>(id) : -1;
+  // Entries of the partition's blocks that exist in the table row (<= 0 when the partition starts
+  // past the row; the context-length check below then ends the workgroup).
+  const int slice = min(((p0 + P - 1) >> lb) - blk0 + 1, p.max_blocks - blk0);
+  const int64_t table_row = static_cast<int64_t>(b) * p.max_blocks + blk0;
+  const bool is64 = p.index_is64 != 0;
+  const RawIndex ctx_raw = load_raw_index(p.context_lengths, b, is64);
+  RawIndex ids[2] = {{~0u, ~0u}, {~0u, ~0u}};  // entries tid and tid + kThreads (a slice has <= 257)
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + i * kThreads;
+    if (idx < slice) ids[i] = load_raw_index(p.block_tables, table_row + idx, is64);
   }
 
   // Query operands.
@@ -311,7 +402,52 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
       }
     }
   }
-  __syncthreads();
+
+  // Block ids of this wave's first DEPTH tiles (tokens p0 + 16 * wave + 64 * n), read straight from
+  // the table so they can be issued before the staged slice is visible to the wave.
+  RawIndex first_raw[2] = {{~0u, ~0u}, {~0u, ~0u}};
+  if constexpr (UB) {
+#pragma unroll
+    for (int n = 0; n < DEPTH; ++n) {
+      const int idx = ((p0 + wave * kTile + n * kWaves * kTile) >> lb) - blk0;
+      if (idx < slice) first_raw[n] = load_raw_index(p.block_tables, table_row + idx, is64);
+    }
+  }
+  auto valid_block = [&](RawIndex r) -> int {
+    const int64_t id = index_value(r, is64);
+    return (id >= 0 && id < p.num_blocks) ? static_cast<int>(id) : -1;
+  };
+
+  const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << lb;
+  const int64_t ctx_len = index_value(ctx_raw, is64);
+  const int64_t ctx = ctx_len < max_ctx ? ctx_len : max_ctx;
+  if (ctx <= 0) {
+    // Softmax over an empty set: NaN, as the fallback produces.  Partition 0 owns the output.
+    if (part == 0) {
+      for (int idx = tid; idx < heads_here * D; idx += kThreads) {
+        const int h = idx / D, d = idx % D;
+        p.out[(static_cast<int64_t>(b) * p.query_heads + head0 + h) * D + d] =
+            E::store(__builtin_nanf(""));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
+  }
+  const int np = static_cast<int>((ctx + P - 1) / P);
+  if (part >= np) {
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
+  }
+  const int p_end = static_cast<int>(min(static_cast<int64_t>(p0 + P), ctx));
+
+  // Stage this partition's block-table slice in LDS (-1 marks ids outside [0, num_blocks)).  It is
+  // made visible by the barrier in front of the main loop.
+  const int nblk = ((p_end - 1) >> lb) - blk0 + 1;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + i * kThreads;
+    if (idx < nblk) s_table[idx] = valid_block(ids[i]);
+  }
 
   const uint16_t* __restrict__ kbase = p.k + static_cast<int64_t>(kvh) * D;
   const uint16_t* __restrict__ vbase = p.v + static_cast<int64_t>(kvh) * D;
@@ -343,16 +479,18 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   const int dma_row = lane / CPR;  // row (within RPI) a lane moves in each K DMA instruction
   const int dma_pos = lane % CPR;  // its 16-byte position in the staged row
   int32_t kdma_off[QK_MFMA ? KSTEPS : 1];
-  int kread[QK_MFMA ? KSTEPS : 1];
+  uint32_t kread[QK_MFMA ? KSTEPS : 1];  // LDS byte address of this lane's operand chunk, slot 0
   if constexpr (QK_MFMA) {
 #pragma unroll
     for (int n = 0; n < KSTEPS; ++n) {
       const int row = RPI * n + dma_row;
       kdma_off[n] = row * row_stride32 + ((dma_pos ^ (row & SWZ)) << 3);
     }
+    const uint32_t k_lds = lds_address(s_k);
 #pragma unroll
-    for (int i = 0; i < KSTEPS; ++i) kread[i] = j * CPR + ((4 * i + g) ^ (j & SWZ));
+    for (int i = 0; i < KSTEPS; ++i) kread[i] = k_lds + 16u * (j * CPR + ((4 * i + g) ^ (j & SWZ)));
   }
+  const uint32_t table_lds = lds_address(s_table);
 
   auto load_v_rows = [&](uint32_t (&dst)[4][VW], const uint16_t* const src[4]) {
 #pragma unroll
@@ -374,11 +512,11 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 
   // Issue every load of the tile starting at token t0: K into LDS slot `slot` (MFMA variant) or
   // registers (VALU variant), V into registers.
-  auto issue_tile = [&](Tile& tile, int slot, int t0) {
+  // Uniform-block form: `pb` is the tile's block id (-1 when invalid).
+  auto issue_tile_block = [&](Tile& tile, int slot, int t0, int pb) {
     const uint16_t* vrow[4];
     const uint16_t* krow[4];
     if constexpr (UB) {
-      const int pb = __builtin_amdgcn_readfirstlane(s_table[(t0 >> lb) - blk0]);
       const bool block_ok = pb >= 0;
       const int64_t base = static_cast<int64_t>(block_ok ? pb : 0) * p.block_stride +
                            static_cast<int64_t>(t0 & bs_mask) * p.row_stride;
@@ -423,6 +561,14 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     if constexpr (!QK_MFMA) load_v_rows(tile.kr, krow);  // K rows of masked tokens need no zeroing
     load_v_rows(tile.v, vrow);
   };
+  auto issue_tile = [&](Tile& tile, int slot, int t0) {
+    int pb = -1;
+    if constexpr (UB) {
+      const int t_tab = min(t0, last);  // a tile past the partition end reads a valid table entry
+      pb = __builtin_amdgcn_readfirstlane(lds_read_i32_sync(table_lds + 4u * ((t_tab >> lb) - blk0)));
+    }
+    issue_tile_block(tile, slot, t0, pb);
+  };
 
   // Online-softmax state.  m_own / l_own belong to head my_head (identical across lane groups
   // after the per-tile reductions); acc covers every head of the chunk for this lane's columns.
@@ -437,13 +583,22 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 
   // Scores of tokens 4g..4g+3 for head my_head, base-2 scaled, -inf where masked.  Branch-free
   // (the full-tile shortcut is a select) so no control flow sits between the tile's wait and its use.
-  auto qk_phase = [&](const Tile& tile, int slot, float (&x)[4]) {
+  auto qk_phase = [&](const Tile& tile, auto slot_tag, float (&x)[4]) {
     const bool FULL = tile.full;
     if constexpr (QK_MFMA) {
-      const u32x4* src = s_k + slot * KTILE16;
+      constexpr int OFFSET = decltype(slot_tag)::value * SLOT_BYTES;
+      u32x4 kop[KSTEPS];
+      if constexpr (KSTEPS == 2) {
+        lds_read2x16_sync<OFFSET>(kop[0], kop[1], kread[0], kread[1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < KSTEPS; i += 4)
+          lds_read4x16_sync<OFFSET>(kop[i], kop[i + 1], kop[i + 2], kop[i + 3], kread[i], kread[i + 1],
+                                    kread[i + 2], kread[i + 3]);
+      }
       f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < KSTEPS; ++i) s = E::mfma(src[kread[i]], qB[i], s);
+      for (int i = 0; i < KSTEPS; ++i) s = E::mfma(kop[i], qB[i], s);
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] = (FULL || ((tile.valid >> r) & 1u)) ? s[r] * p.scale_log2e : neg_inf;
     } else {
@@ -533,45 +688,93 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     }
   };
 
-  // One tile: wait for `cur`, compute its scores, send out the next tile's loads (if any), then
-  // softmax and PV of `cur` while they are in flight.  Slots and the has-next choice are
-  // compile-time tags so the register tiles stay in registers.
+  // One tile: wait until `cur` has landed, send out the loads of the tile DEPTH steps ahead (if
+  // any), then scores, softmax and PV of `cur` while those loads are in flight.  Slots, the
+  // has-next choice and the number of tiles still allowed in flight are compile-time tags, so the
+  // register tiles stay in registers and every wait is exact.
   //
-  // The wait is explicit: at this point the only memory operations in flight are `cur`'s own (its
-  // K DMA into LDS and its V register loads), so waiting for all of them costs nothing extra, and
-  // it is the wait the LDS reads of the DMA'd K tile need.  The compiler's own counter tracking
-  // does not model LDS-DMA completion precisely; with this unconditional wait ahead of every use
-  // it never has to (and emits no later wait that would also stall on the next tile's loads).
-  auto step = [&](const Tile& cur, auto cur_slot, Tile& next, auto next_slot, int next_t0, auto has_next) {
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  // The wait is explicit.  Loads retire in issue order, so waiting until at most PENDING tiles'
+  // worth of operations is outstanding (PENDING = tiles issued after `cur`) is exactly the wait for
+  // `cur`'s K DMA and V loads.  The compiler's own counter tracking does not model LDS-DMA completion
+  // precisely; with this wait ahead of every use it never has to.  The slot and register tile that
+  // the new loads overwrite belong to the tile computed in the previous step, which is finished.
+  auto step = [&](const Tile& cur, auto cur_slot, Tile& next, auto next_slot, int next_t0, auto has_next,
+                  auto pending) {
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(decltype(pending)::value * TILE_OPS));
     __asm__ __volatile__("" ::: "memory");
-    float x[4];
-    qk_phase(cur, decltype(cur_slot)::value, x);
     if constexpr (decltype(has_next)::value) issue_tile(next, decltype(next_slot)::value, next_t0);
+    float x[4];
+    qk_phase(cur, cur_slot, x);
     if (cur.full)
       pv_phase(cur, x, Flag<true>{});
     else
       pv_phase(cur, x, Flag<false>{});
   };
 
-  // Tiles of this wave: t0 = first + n * step_tokens, n < n_tiles.  Two register tiles (and two
-  // LDS K slots) alternate; the loop is peeled so that every load it issues is unconditional.
+  // Tiles of this wave: t0 = first + n * step_tokens, n < n_tiles; tile n uses slot n % SLOTS.  The
+  // loop is peeled so that every load it issues is unconditional.
   const int step_tokens = kWaves * kTile;
   const int first = p0 + wave * kTile;
   const int n_tiles = first < p_end ? (p_end - first + step_tokens - 1) / step_tokens : 0;
-  Tile ta, tb;
-  if (n_tiles > 0) {
-    issue_tile(ta, 0, first);
-    int n = 0;
-    for (; n + 2 < n_tiles; n += 2) {
-      step(ta, Int<0>{}, tb, Int<1>{}, first + (n + 1) * step_tokens, Flag<true>{});
-      step(tb, Int<1>{}, ta, Int<0>{}, first + (n + 2) * step_tokens, Flag<true>{});
+  auto t0_of = [&](int n) { return first + n * step_tokens; };
+  constexpr Flag<true> kIssue{};
+  constexpr Flag<false> kNoIssue{};
+  Tile ta, tb, tc;
+  // The first DEPTH tiles go out before the barrier that publishes the staged table (uniform-block
+  // path: their block ids were read directly).  With DEPTH 2 the second tile is issued even when it
+  // does not exist (its tokens then read as masked stand-ins of the first tile's block and it is
+  // never computed): an unconditional issue keeps the compiler's view of the memory counter
+  // identical on every path into the loop, so it adds no waits of its own.
+  if constexpr (UB) {
+    if (n_tiles > 0) {
+      const int pb0 = valid_block(first_raw[0]);
+      issue_tile_block(ta, 0, t0_of(0), pb0);
+      if constexpr (DEPTH == 2) issue_tile_block(tb, 1, t0_of(1), t0_of(1) <= last ? valid_block(first_raw[1]) : pb0);
     }
-    if (n + 1 < n_tiles) {
-      step(ta, Int<0>{}, tb, Int<1>{}, first + (n + 1) * step_tokens, Flag<true>{});
-      step(tb, Int<1>{}, ta, Int<0>{}, 0, Flag<false>{});
-    } else {
-      step(ta, Int<0>{}, tb, Int<1>{}, 0, Flag<false>{});
+  }
+  lds_barrier();
+  if constexpr (!UB) {
+    if (n_tiles > 0) issue_tile(ta, 0, t0_of(0));
+  }
+  if constexpr (DEPTH == 2) {
+    if (n_tiles > 0) {
+      int n = 0;
+      for (; n + 5 <= n_tiles; n += 3) {
+        step(ta, Int<0>{}, tc, Int<2>{}, t0_of(n + 2), kIssue, Int<1>{});
+        step(tb, Int<1>{}, ta, Int<0>{}, t0_of(n + 3), kIssue, Int<1>{});
+        step(tc, Int<2>{}, tb, Int<1>{}, t0_of(n + 4), kIssue, Int<1>{});
+      }
+      // 1 to 4 tiles remain; tiles n and n + 1 (if it exists) are already in flight.
+      const int left = n_tiles - n;
+      if (left == 1) {
+        step(ta, Int<0>{}, tc, Int<2>{}, 0, kNoIssue, Int<0>{});
+      } else if (left == 2) {
+        step(ta, Int<0>{}, tc, Int<2>{}, 0, kNoIssue, Int<1>{});
+        step(tb, Int<1>{}, ta, Int<0>{}, 0, kNoIssue, Int<0>{});
+      } else if (left == 3) {
+        step(ta, Int<0>{}, tc, Int<2>{}, t0_of(n + 2), kIssue, Int<1>{});
+        step(tb, Int<1>{}, ta, Int<0>{}, 0, kNoIssue, Int<1>{});
+        step(tc, Int<2>{}, tb, Int<1>{}, 0, kNoIssue, Int<0>{});
+      } else {
+        step(ta, Int<0>{}, tc, Int<2>{}, t0_of(n + 2), kIssue, Int<1>{});
+        step(tb, Int<1>{}, ta, Int<0>{}, t0_of(n + 3), kIssue, Int<1>{});
+        step(tc, Int<2>{}, tb, Int<1>{}, 0, kNoIssue, Int<1>{});
+        step(ta, Int<0>{}, tc, Int<2>{}, 0, kNoIssue, Int<0>{});
+      }
+    }
+  } else {
+    if (n_tiles > 0) {
+      int n = 0;
+      for (; n + 2 < n_tiles; n += 2) {
+        step(ta, Int<0>{}, tb, Int<1>{}, t0_of(n + 1), kIssue, Int<0>{});
+        step(tb, Int<1>{}, ta, Int<0>{}, t0_of(n + 2), kIssue, Int<0>{});
+      }
+      if (n + 1 < n_tiles) {
+        step(ta, Int<0>{}, tb, Int<1>{}, t0_of(n + 1), kIssue, Int<0>{});
+        step(tb, Int<1>{}, ta, Int<0>{}, 0, kNoIssue, Int<0>{});
+      } else {
+        step(ta, Int<0>{}, tb, Int<1>{}, 0, kNoIssue, Int<0>{});
+      }
     }
   }
 
@@ -871,7 +1074,11 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   const int64_t group = query_heads / kv_heads;
   const int gc = head_chunk_for(group);
   const int64_t head_chunks = (group + gc - 1) / gc;
-  const int64_t grid = batch * kv_heads * head_chunks * s.num_partitions;
+  // Padded to whole rounds of (8 XCDs x head slots); the kernel maps hardware ids onto work items.
+  const int64_t xcd_round = kXcds * kv_heads * head_chunks;
+  const int64_t items = batch * kv_heads * head_chunks * s.num_partitions;
+  const bool xcd_grouped = items >= kXcdGroupedItems;
+  const int64_t grid = xcd_grouped ? (items + xcd_round - 1) / xcd_round * xcd_round : items;
   if (grid >= (int64_t{1} << 31))
     return fail(RK_ERR_UNSUPPORTED, "launch grid exceeds 2^31 workgroups");
 
@@ -900,6 +1107,7 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.bs_log2 = log2_exact(block_size);
   prm.partition_tokens = static_cast<int32_t>(partition_tokens);
   prm.num_partitions = static_cast<int32_t>(s.num_partitions);
+  prm.xcd_grouped = xcd_grouped ? 1 : 0;
   prm.index_is64 = index_dtype == RK_INDEX_INT64 ? 1 : 0;
   prm.scale_log2e = scale * kLog2e;
 

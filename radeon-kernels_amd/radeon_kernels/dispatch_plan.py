@@ -42,19 +42,19 @@ EXACT_REGIONS: list[tuple[str, dict[str, Any], dict[str, Any]]] = [
         "b8-gqa32x8-c1024-d128-p16-bf16",
         {"dtype": "bf16", "batch": 8, "query_heads": 32, "kv_heads": 8, "head_dim": 128, "num_blocks": 1024,
          "block_size": 16, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 64},
+        {"partition_tokens": 256},
     ),
     (
         "b4-mha16-c2048-d64-p32-bf16",
         {"dtype": "bf16", "batch": 4, "query_heads": 16, "kv_heads": 16, "head_dim": 64, "num_blocks": 512,
          "block_size": 32, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 128},
+        {"partition_tokens": 512},
     ),
     (
         "b4-gqa32x8-c1024-d256-p16-fp16",
         {"dtype": "fp16", "batch": 4, "query_heads": 32, "kv_heads": 8, "head_dim": 256, "num_blocks": 512,
          "block_size": 16, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 64},
+        {"partition_tokens": 128},
     ),
     (
         "b128-gqa32x8-ragged-d128-p16-bf16",

@@ -1,15 +1,18 @@
-"""Build the gfx950 paged-attention decode library and its repo-local kernel pack.
+"""Build the gfx950 kernel libraries and their repo-local kernel pack.
 
 Outputs (all under ``radeon-kernels_amd/packs/gfx950``):
 
-* ``lib/librk_pa_gfx950.so`` -- the C-ABI library (``include/rk_paged_attention.h``), HIP for gfx950.
-* ``lib/rk_pa_gfx950.so``    -- the PyTorch-ROCm binding (module ``rk_pa_gfx950``) that dispatch
-  entries load as a ``python_extension`` artifact.
+* ``lib/librk_pa_gfx950.so`` -- paged-attention decode C-ABI library (``include/rk_paged_attention.h``).
+* ``lib/rk_pa_gfx950.so``    -- its PyTorch-ROCm binding (module ``rk_pa_gfx950``).
+* ``lib/librk_kv_gfx950.so`` -- paged KV-cache C-ABI library (``include/rk_kv_cache.h``).
+* ``lib/rk_kv_gfx950.so``    -- its PyTorch-ROCm binding (module ``rk_kv_gfx950``).
 * ``manifest.json``          -- the kernel-pack manifest (same fields as the reference's
-  ``schemas/kernel-pack.schema.json``), stamped with the binding's SHA-256 and this environment.
+  ``schemas/kernel-pack.schema.json``), stamped with the bindings' SHA-256 and this environment.
 
-It also rewrites the winners' ``sha256`` and ``environment`` in
-``radeon_kernels/dispatch/paged_attention_decode-1.0.json`` from ``dispatch_plan.py``.  The
+Dispatch entries load the bindings as ``python_extension`` artifacts; each binding carries the
+SHA-256 of the library it links and refuses to import against any other.  The build also rewrites
+the winners' ``sha256`` and ``environment`` in ``radeon_kernels/dispatch/<operator>-1.0.json`` from
+``dispatch_plan.py``.  The
 reference binds every dispatch entry to the exact artifact digest and to the exact
 torch/Python/ROCm ABI (src/radeon_kernels/runtime/compatibility.py:94-102), so both files are
 generated after each build rather than written by hand.
@@ -103,81 +106,104 @@ def sha256_file(path: Path) -> str:
     return digest.hexdigest()
 
 
-def compile_libraries(verbose: bool = False) -> tuple[Path, Path]:
-    """Compile the C-ABI library (hipcc) and the torch binding (g++); return their paths."""
+class Library:
+    """One C-ABI kernel library (hipcc) plus the torch binding (g++) that links against it."""
 
-    import torch  # noqa: F401  (paths and ABI flag come from the installed torch)
+    def __init__(self, operator: str, hip_source: str, cabi_name: str, binding_source: str, module: str,
+                 digest_symbol: str) -> None:
+        self.operator = operator
+        self.hip_source = CSRC / hip_source
+        self.cabi_name = cabi_name
+        self.binding_source = CSRC / binding_source
+        self.module = module
+        self.digest_symbol = digest_symbol
+
+
+LIBRARIES = (
+    Library("paged_attention_decode", "pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", EXTENSION_NAME,
+            "kRkKernelLibrarySha256"),
+    Library("kv_cache_append", "kv_cache_gfx950.hip", "librk_kv_gfx950.so", "kv_torch_ext.cpp", "rk_kv_gfx950",
+            "kRkKvLibrarySha256"),
+)
+
+
+def compile_libraries(verbose: bool = False) -> dict[str, Path]:
+    """Compile every C-ABI library (hipcc) and torch binding (g++); returns operator -> binding path."""
+
+    import torch
 
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     # A fixed build directory keeps the output byte-identical across builds: clang derives the
     # offload compilation-unit id from the command line, which includes the output path.
     work = PACKAGE_ROOT / "_build"
     work.mkdir(exist_ok=True)
-    cabi_tmp = work / CABI_NAME
-    ext_obj = work / "pa_torch_ext.o"
-    ext_tmp = work / f"{EXTENSION_NAME}.so"
-
-    hip = _run(
-        [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(CSRC / "pa_decode_gfx950.hip"), "-o", str(cabi_tmp)],
-        verbose,
-    )
     includes, libraries = _torch_paths()
-    import torch
-
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    cxx = [
-        "g++",
-        "-O2",
-        "-std=c++17",
-        "-fPIC",
-        "-c",
-        "-D__HIP_PLATFORM_AMD__=1",
-        "-DUSE_ROCM=1",
-        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
-        f"-DTORCH_EXTENSION_NAME={EXTENSION_NAME}",
-        "-DTORCH_API_INCLUDE_EXTENSION_H",
-        f"-ffile-prefix-map={REPO_ROOT}=.",
-        *[f"-I{path}" for path in includes],
-        f"-I{sysconfig.get_paths()['include']}",
-        f"-I{INCLUDE}",
-        str(CSRC / "pa_torch_ext.cpp"),
-        "-o",
-        str(ext_obj),
-    ]
-    gxx = _run(cxx, verbose)
-    _finish(hip, "hipcc (C-ABI library)")
-    # The binding checks at import that the kernel library it loads is the one built here.
-    digest_src = work / "kernel_digest.cpp"
-    digest_obj = work / "kernel_digest.o"
-    digest_src.write_text(f'extern const char kRkKernelLibrarySha256[] = "{sha256_file(cabi_tmp)}";\n')
-    _finish(_run(["g++", "-O2", "-fPIC", "-c", str(digest_src), "-o", str(digest_obj)], verbose),
-            "g++ (kernel library digest)")
-    _finish(gxx, "g++ (torch binding)")
-    link = [
-        "g++",
-        "-shared",
-        str(ext_obj),
-        str(digest_obj),
-        f"-L{work}",
-        *[f"-L{path}" for path in libraries],
-        "-l:" + CABI_NAME,
-        "-lc10",
-        "-lc10_hip",
-        "-ltorch",
-        "-ltorch_cpu",
-        "-ltorch_hip",
-        "-ltorch_python",
-        "-Wl,-rpath,$ORIGIN",
-        "-Wl,--build-id=none",
-        "-o",
-        str(ext_tmp),
-    ]
-    _finish(_run(link, verbose), "link (torch binding)")
-    os.replace(cabi_tmp, LIB_DIR / CABI_NAME)
-    os.replace(ext_tmp, LIB_DIR / f"{EXTENSION_NAME}.so")
-    ext_obj.unlink()
-    digest_obj.unlink()
-    return LIB_DIR / CABI_NAME, LIB_DIR / f"{EXTENSION_NAME}.so"
+
+    # All compilations run concurrently; each binding is linked once its library exists.
+    jobs = []
+    for lib in LIBRARIES:
+        cabi_tmp = work / lib.cabi_name
+        hip = _run([_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(lib.hip_source), "-o", str(cabi_tmp)], verbose)
+        ext_obj = work / f"{lib.module}.o"
+        cxx = [
+            "g++",
+            "-O2",
+            "-std=c++17",
+            "-fPIC",
+            "-c",
+            "-D__HIP_PLATFORM_AMD__=1",
+            "-DUSE_ROCM=1",
+            f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            f"-DTORCH_EXTENSION_NAME={lib.module}",
+            "-DTORCH_API_INCLUDE_EXTENSION_H",
+            f"-ffile-prefix-map={REPO_ROOT}=.",
+            *[f"-I{path}" for path in includes],
+            f"-I{sysconfig.get_paths()['include']}",
+            f"-I{INCLUDE}",
+            str(lib.binding_source),
+            "-o",
+            str(ext_obj),
+        ]
+        jobs.append((lib, cabi_tmp, ext_obj, hip, _run(cxx, verbose)))
+
+    bindings: dict[str, Path] = {}
+    for lib, cabi_tmp, ext_obj, hip, gxx in jobs:
+        _finish(hip, f"hipcc ({lib.cabi_name})")
+        # The binding checks at import that the kernel library it loads is the one built here.
+        digest_src = work / f"{lib.module}_digest.cpp"
+        digest_obj = work / f"{lib.module}_digest.o"
+        digest_src.write_text(f'extern const char {lib.digest_symbol}[] = "{sha256_file(cabi_tmp)}";\n')
+        _finish(_run(["g++", "-O2", "-fPIC", "-c", str(digest_src), "-o", str(digest_obj)], verbose),
+                f"g++ ({lib.module} library digest)")
+        _finish(gxx, f"g++ ({lib.module} binding)")
+        ext_tmp = work / f"{lib.module}.so"
+        link = [
+            "g++",
+            "-shared",
+            str(ext_obj),
+            str(digest_obj),
+            f"-L{work}",
+            *[f"-L{path}" for path in libraries],
+            "-l:" + lib.cabi_name,
+            "-lc10",
+            "-lc10_hip",
+            "-ltorch",
+            "-ltorch_cpu",
+            "-ltorch_hip",
+            "-ltorch_python",
+            "-Wl,-rpath,$ORIGIN",
+            "-Wl,--build-id=none",
+            "-o",
+            str(ext_tmp),
+        ]
+        _finish(_run(link, verbose), f"link ({lib.module} binding)")
+        os.replace(cabi_tmp, LIB_DIR / lib.cabi_name)
+        os.replace(ext_tmp, LIB_DIR / f"{lib.module}.so")
+        ext_obj.unlink()
+        digest_obj.unlink()
+        bindings[lib.operator] = LIB_DIR / f"{lib.module}.so"
+    return bindings
 
 
 def environment_record() -> dict:
@@ -197,24 +223,25 @@ def environment_record() -> dict:
     }
 
 
-def write_pack_and_dispatch(extension: Path) -> dict:
+def write_pack_and_dispatch(bindings: dict[str, Path]) -> dict:
     sys.path.insert(0, str(PACKAGE_ROOT))
     from radeon_kernels.dispatch_plan import render_dispatch_manifest, render_pack_manifest
 
-    digest = sha256_file(extension)
+    digests = {operator: sha256_file(path) for operator, path in bindings.items()}
     environment = environment_record()
-    artifact = f"lib/{extension.name}"
-    pack = render_pack_manifest(environment=environment, artifact=artifact, sha256=digest)
+    pack = render_pack_manifest(environment=environment, digests=digests)
     _atomic_write(PACK_DIR / "manifest.json", json.dumps(pack, indent=2, sort_keys=True) + "\n")
-    dispatch = render_dispatch_manifest(environment=environment, artifact=artifact, sha256=digest)
-    target = PACKAGE_ROOT / "radeon_kernels" / "dispatch" / "paged_attention_decode-1.0.json"
-    _atomic_write(target, json.dumps(dispatch, indent=2, sort_keys=True) + "\n")
-    return {"sha256": digest, "environment": environment, "entries": len(dispatch["entries"])}
+    entries = {}
+    for operator, digest in digests.items():
+        dispatch = render_dispatch_manifest(operator, environment=environment, sha256=digest)
+        target = PACKAGE_ROOT / "radeon_kernels" / "dispatch" / f"{operator}-1.0.json"
+        _atomic_write(target, json.dumps(dispatch, indent=2, sort_keys=True) + "\n")
+        entries[operator] = len(dispatch["entries"])
+    return {"sha256": digests, "environment": environment, "entries": entries}
 
 
 def build(verbose: bool = False) -> dict:
-    _, extension = compile_libraries(verbose=verbose)
-    summary = write_pack_and_dispatch(extension)
+    summary = write_pack_and_dispatch(compile_libraries(verbose=verbose))
     if verbose:
         print(json.dumps(summary, indent=2), flush=True)
     return summary

@@ -1,0 +1,135 @@
+// Paged KV-cache append for MI355X (gfx950, CDNA4, wave64).
+//
+// Operator semantics follow the reference fallback (src/radeon_kernels/ops/kv_cache/reference.py:6-20)
+// and contract (contracts/kv_cache_append-1.0.json:15-22): token t's K row and V row, each
+// kv_heads * head_dim contiguous elements, are copied bit for bit to physical slot slot_mapping[t]
+// of the [num_blocks * block_size, kv_heads, head_dim] view of the caches.  A slot outside the
+// cache is skipped, as the reference's own kernel does (benchmarks/kv_cache/native_kv_cache.hip:42-45).
+//
+// A K/V row is the unit both sides share: contiguous in the token tensors and contiguous in the
+// cache (one slot of one block).  So the kernel is a row gather/scatter of 16-byte chunks:
+//
+//   kv_append_kernel  one workgroup per (token, run of up to 256 chunks of its row).  The slot is
+//                     wave-uniform (one token per workgroup), read once by a scalar load; every
+//                     lane moves the same 16-byte chunk of the K row and of the V row, so both
+//                     loads and both stores are fully coalesced 1 KB wave transactions.  The slot
+//                     load and the two data loads are independent and go out together.
+//
+// Algorithmic bytes: 4 * tokens * kv_heads * head_dim * 2 (read K and V, write K and V) plus the
+// slot indices; it is an HBM-bound copy with no arithmetic.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "rk_kv_cache.h"
+
+namespace {
+
+constexpr int kMaxThreads = 256;
+constexpr int kChunk = 16;  // bytes per lane per row
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct AppendParams {
+  const u32x4* key;
+  const u32x4* value;
+  u32x4* key_cache;
+  u32x4* value_cache;
+  const void* slots;
+  int64_t capacity;     // num_blocks * block_size
+  int32_t row_chunks;   // 16-byte chunks per token row (kv_heads * head_dim * 2 / 16)
+  int32_t row_blocks;   // workgroups per token row
+  int32_t index_is64;
+};
+
+__global__ __launch_bounds__(kMaxThreads) void kv_append_kernel(AppendParams p) {
+  // blockIdx.x = token * row_blocks + run; the division is on wave-uniform values.
+  const int token = static_cast<int>(blockIdx.x) / p.row_blocks;
+  const int run = static_cast<int>(blockIdx.x) - token * p.row_blocks;
+  const int chunk = run * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+  const int64_t slot = p.index_is64 ? static_cast<const int64_t*>(p.slots)[token]
+                                    : static_cast<int64_t>(static_cast<const int32_t*>(p.slots)[token]);
+  if (chunk >= p.row_chunks) return;
+  const int64_t src = static_cast<int64_t>(token) * p.row_chunks + chunk;
+  const u32x4 k = p.key[src];
+  const u32x4 v = p.value[src];
+  if (slot < 0 || slot >= p.capacity) return;
+  const int64_t dst = slot * p.row_chunks + chunk;
+  p.key_cache[dst] = k;
+  p.value_cache[dst] = v;
+}
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buffer[512];
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(buffer, sizeof(buffer), fmt, args);
+  va_end(args);
+  g_last_error = buffer;
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int rk_kv_cache_append(const void* key, const void* value, void* key_cache,
+                                  void* value_cache, const void* slot_mapping, int64_t tokens,
+                                  int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
+                                  int64_t block_size, int dtype, int index_dtype, void* stream) {
+  if (key == nullptr || value == nullptr || key_cache == nullptr || value_cache == nullptr ||
+      slot_mapping == nullptr)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "tensor pointers must not be NULL");
+  if (dtype != RK_KV_DTYPE_FP16 && dtype != RK_KV_DTYPE_BF16)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (index_dtype != RK_KV_INDEX_INT32 && index_dtype != RK_KV_INDEX_INT64)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "unknown index_dtype %d", index_dtype);
+  if (tokens <= 0 || kv_heads <= 0 || head_dim <= 0 || num_blocks <= 0 || block_size <= 0)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "tensor dimensions must be positive");
+  if (!aligned16(key) || !aligned16(value) || !aligned16(key_cache) || !aligned16(value_cache))
+    return fail(RK_KV_ERR_UNSUPPORTED, "key, value and caches must be 16-byte aligned");
+  const int64_t row_bytes = kv_heads * head_dim * 2;
+  if (row_bytes % kChunk != 0)
+    return fail(RK_KV_ERR_UNSUPPORTED,
+                "kv_heads * head_dim * 2 must be a multiple of 16 bytes (got %lld)",
+                static_cast<long long>(row_bytes));
+  const int64_t row_chunks = row_bytes / kChunk;
+  // Token-side chunk indices fit in 32 bits; cache-side ones (slot * row_chunks) in 50.
+  if (tokens * row_chunks >= (int64_t{1} << 31) || num_blocks > (int64_t{1} << 50) / block_size ||
+      num_blocks * block_size > (int64_t{1} << 50) / row_chunks)
+    return fail(RK_KV_ERR_UNSUPPORTED, "shape exceeds the index range of this kernel");
+
+  // Workgroup size: whole waves, at most 256 threads, no more than the row needs.
+  const int64_t threads = row_chunks >= kMaxThreads ? kMaxThreads : ((row_chunks + 63) / 64) * 64;
+  const int64_t row_blocks = (row_chunks + threads - 1) / threads;
+  const int64_t grid = tokens * row_blocks;
+  if (grid >= (int64_t{1} << 31))
+    return fail(RK_KV_ERR_UNSUPPORTED, "launch grid exceeds 2^31 workgroups");
+
+  AppendParams prm{};
+  prm.key = static_cast<const u32x4*>(key);
+  prm.value = static_cast<const u32x4*>(value);
+  prm.key_cache = static_cast<u32x4*>(key_cache);
+  prm.value_cache = static_cast<u32x4*>(value_cache);
+  prm.slots = slot_mapping;
+  prm.capacity = num_blocks * block_size;
+  prm.row_chunks = static_cast<int32_t>(row_chunks);
+  prm.row_blocks = static_cast<int32_t>(row_blocks);
+  prm.index_is64 = index_dtype == RK_KV_INDEX_INT64 ? 1 : 0;
+  hipLaunchKernelGGL(kv_append_kernel, dim3(static_cast<uint32_t>(grid)),
+                     dim3(static_cast<uint32_t>(threads)), 0, static_cast<hipStream_t>(stream), prm);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(RK_KV_ERR_LAUNCH, "launch failed: %s", hipGetErrorString(err));
+  return RK_KV_OK;
+}
+
+extern "C" const char* rk_kv_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" const char* rk_kv_version(void) { return "rk_kv_gfx950 1.0.0 (gfx950, wave64)"; }

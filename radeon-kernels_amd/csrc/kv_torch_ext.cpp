@@ -1,0 +1,97 @@
+// PyTorch-ROCm binding of the gfx950 paged KV-cache library (include/rk_kv_cache.h).
+//
+// The python_extension artifact that kv_cache_append dispatch entries name.  Its entrypoint keeps
+// the calling convention of the reference bindings (benchmarks/kv_cache/native_kv_cache.hip:259-283,
+// invoked by src/radeon_kernels/providers/native.py:25 as entrypoint(key, value, key_cache,
+// value_cache, slot_mapping)): it validates, writes the caches in place on the current HIP stream and
+// returns them.  No host synchronisation, no device-to-host reads: safe under HIP graph capture.
+//
+// The kernels live in librk_kv_gfx950.so next to this module.  The build bakes that library's
+// SHA-256 into this module and the import fails unless the library actually loaded has it, so the
+// digest a dispatch entry pins for this module also pins the kernels it runs.
+#include <dlfcn.h>
+#include <torch/extension.h>
+
+#include <c10/hip/HIPStream.h>
+
+#include <string>
+#include <vector>
+
+#include "rk_kv_cache.h"
+
+// Defined in a file the build generates after compiling the kernel library.
+extern const char kRkKvLibrarySha256[];
+
+namespace {
+
+std::string loaded_kernel_library_digest(std::string* path_out) {
+  Dl_info info{};
+  if (dladdr(reinterpret_cast<void*>(&rk_kv_version), &info) == 0 || info.dli_fname == nullptr) {
+    throw py::import_error("rk_kv_gfx950: cannot locate the loaded kernel library");
+  }
+  *path_out = info.dli_fname;
+  py::bytes content = py::module_::import("pathlib").attr("Path")(*path_out).attr("read_bytes")();
+  return py::module_::import("hashlib").attr("sha256")(content).attr("hexdigest")().cast<std::string>();
+}
+
+void check_data(const at::Tensor& t, const char* name, int64_t rank) {
+  TORCH_CHECK_VALUE(t.is_cuda(), name, " must be a ROCm tensor");
+  TORCH_CHECK_VALUE(t.dim() == rank, name, " must be rank ", rank);
+  TORCH_CHECK_VALUE(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK_TYPE(t.scalar_type() == at::kHalf || t.scalar_type() == at::kBFloat16, name,
+                   " must use FP16 or BF16");
+}
+
+std::vector<at::Tensor> append(const at::Tensor& key, const at::Tensor& value, at::Tensor key_cache,
+                               at::Tensor value_cache, const at::Tensor& slot_mapping) {
+  check_data(key, "key", 3);
+  check_data(value, "value", 3);
+  check_data(key_cache, "key_cache", 4);
+  check_data(value_cache, "value_cache", 4);
+  TORCH_CHECK_VALUE(slot_mapping.is_cuda() && slot_mapping.dim() == 1 && slot_mapping.is_contiguous(),
+                    "slot_mapping must be a contiguous rank-1 ROCm tensor");
+  TORCH_CHECK_TYPE(slot_mapping.scalar_type() == at::kInt || slot_mapping.scalar_type() == at::kLong,
+                   "slot_mapping must use INT32 or INT64");
+  const auto device = key.device();
+  TORCH_CHECK_VALUE(value.device() == device && key_cache.device() == device &&
+                        value_cache.device() == device && slot_mapping.device() == device,
+                    "all tensors must be on the key device");
+  TORCH_CHECK_TYPE(value.scalar_type() == key.scalar_type() &&
+                       key_cache.scalar_type() == key.scalar_type() &&
+                       value_cache.scalar_type() == key.scalar_type(),
+                   "key, value and cache dtypes must match");
+  TORCH_CHECK_VALUE(key.sizes() == value.sizes(), "key and value shapes must match");
+  TORCH_CHECK_VALUE(key_cache.sizes() == value_cache.sizes(), "cache shapes must match");
+  TORCH_CHECK_VALUE(key.size(0) == slot_mapping.size(0), "slot_mapping must match tokens");
+  TORCH_CHECK_VALUE(key.size(1) == key_cache.size(2) && key.size(2) == key_cache.size(3),
+                    "key/value shape must match cache heads and head dimension");
+  c10::DeviceGuard guard(device);
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(device.index()).stream();
+  const int status = rk_kv_cache_append(
+      key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+      slot_mapping.data_ptr(), key.size(0), key.size(1), key.size(2), key_cache.size(0),
+      key_cache.size(1), key.scalar_type() == at::kBFloat16 ? RK_KV_DTYPE_BF16 : RK_KV_DTYPE_FP16,
+      slot_mapping.scalar_type() == at::kLong ? RK_KV_INDEX_INT64 : RK_KV_INDEX_INT32, stream);
+  if (status == RK_KV_ERR_INVALID_ARGUMENT || status == RK_KV_ERR_UNSUPPORTED) {
+    TORCH_CHECK_VALUE(false, "rk_kv_gfx950: ", rk_kv_last_error());
+  }
+  TORCH_CHECK(status == RK_KV_OK, "rk_kv_gfx950: ", rk_kv_last_error());
+  return {key_cache, value_cache};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(rk_kv_gfx950, module) {
+  module.doc() = "gfx950 paged KV-cache append (16-byte row-chunk gather/scatter)";
+  std::string library_path;
+  const std::string digest = loaded_kernel_library_digest(&library_path);
+  if (digest != kRkKvLibrarySha256) {
+    throw py::import_error("rk_kv_gfx950: kernel library " + library_path + " has SHA-256 " + digest +
+                           ", this module was built against " + kRkKvLibrarySha256);
+  }
+  module.attr("kernel_library") = library_path;
+  module.attr("kernel_library_sha256") = digest;
+  module.def("append", &append, "append token K/V rows to their paged-cache slots", py::arg("key"),
+             py::arg("value"), py::arg("key_cache"), py::arg("value_cache"), py::arg("slot_mapping"));
+  module.def("version", []() { return std::string(rk_kv_version()); });
+}

@@ -138,3 +138,77 @@ def library() -> PagedAttentionLibrary:
     if _LIBRARY is None:
         _LIBRARY = PagedAttentionLibrary()
     return _LIBRARY
+
+
+# ---------------------------------------------------------------------------------------------
+# Paged KV-cache library (include/rk_kv_cache.h).
+KV_LIBRARY_PATH = LIBRARY_PATH.parent / "librk_kv_gfx950.so"
+KV_EXPORTED_SYMBOLS = ("rk_kv_cache_append", "rk_kv_last_error", "rk_kv_version")
+RK_KV_OK = 0
+RK_KV_ERR_INVALID_ARGUMENT = 1
+RK_KV_ERR_UNSUPPORTED = 2
+RK_KV_ERR_LAUNCH = 4
+
+
+class KvCacheLibrary:
+    def __init__(self, path: Path | str | None = None) -> None:
+        import torch  # noqa: F401  (bind to torch's HIP runtime, see module docstring)
+
+        self.path = Path(path) if path is not None else KV_LIBRARY_PATH
+        if not self.path.is_file():
+            raise FileNotFoundError(
+                f"native library {self.path} is missing; build it with `python radeon-kernels_amd/build.py`"
+            )
+        lib = ctypes.CDLL(str(self.path))
+        i64, vp = ctypes.c_int64, ctypes.c_void_p
+        lib.rk_kv_cache_append.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int, ctypes.c_int, vp]
+        lib.rk_kv_cache_append.restype = ctypes.c_int
+        lib.rk_kv_last_error.argtypes = []
+        lib.rk_kv_last_error.restype = ctypes.c_char_p
+        lib.rk_kv_version.argtypes = []
+        lib.rk_kv_version.restype = ctypes.c_char_p
+        self.lib = lib
+
+    def version(self) -> str:
+        return self.lib.rk_kv_version().decode()
+
+    def last_error(self) -> str:
+        return self.lib.rk_kv_last_error().decode()
+
+    def append_raw(self, *, key: int, value: int, key_cache: int, value_cache: int, slot_mapping: int, tokens: int,
+                   kv_heads: int, head_dim: int, num_blocks: int, block_size: int, dtype: int, index_dtype: int,
+                   stream: int) -> int:
+        return self.lib.rk_kv_cache_append(key, value, key_cache, value_cache, slot_mapping, tokens, kv_heads,
+                                           head_dim, num_blocks, block_size, dtype, index_dtype, stream or None)
+
+    def append(self, key: Any, value: Any, key_cache: Any, value_cache: Any, slot_mapping: Any, *,
+               stream: Any | None = None) -> tuple[Any, Any]:
+        """Launch on torch tensors (all on one GPU); writes the caches in place and returns them."""
+
+        import torch
+
+        tokens, kv_heads, head_dim = (int(s) for s in key.shape)
+        num_blocks, block_size = int(key_cache.shape[0]), int(key_cache.shape[1])
+        if stream is None:
+            stream = torch.cuda.current_stream(key.device)
+        status = self.append_raw(
+            key=key.data_ptr(), value=value.data_ptr(), key_cache=key_cache.data_ptr(),
+            value_cache=value_cache.data_ptr(), slot_mapping=slot_mapping.data_ptr(), tokens=tokens,
+            kv_heads=kv_heads, head_dim=head_dim, num_blocks=num_blocks, block_size=block_size,
+            dtype=RK_DTYPE_BF16 if key.dtype == torch.bfloat16 else RK_DTYPE_FP16,
+            index_dtype=RK_INDEX_INT64 if slot_mapping.dtype == torch.int64 else RK_INDEX_INT32,
+            stream=stream.cuda_stream,
+        )
+        if status != RK_KV_OK:
+            raise CabiError(status, self.last_error())
+        return key_cache, value_cache
+
+
+_KV_LIBRARY: KvCacheLibrary | None = None
+
+
+def kv_library() -> KvCacheLibrary:
+    global _KV_LIBRARY
+    if _KV_LIBRARY is None:
+        _KV_LIBRARY = KvCacheLibrary()
+    return _KV_LIBRARY

@@ -5,15 +5,17 @@ The reference binds each dispatch entry to the exact artifact digest and environ
 build stamps those two fields into the documents produced here.  Everything else -- which workload
 regions get which entrypoint and launch parameters -- is this table.
 
-Regions:
+Operators and regions:
 
-* one exact entry (priority 100) per measured workload shape, with the partition size chosen for
-  that shape (``launch.partition_tokens``);
-* one broad gfx950 region (priority 10) covering every shape the library accepts, so any other
-  gfx950 request also runs natively; shapes the kernel rejects at launch time (a ValueError) are
-  demoted to the torch fallback by the runtime with the reason recorded.
+* ``paged_attention_decode``: one exact entry (priority 100) per measured workload shape, with the
+  partition size chosen for that shape (``launch.partition_tokens``), and one broad gfx950 region
+  (priority 10) covering every shape the library accepts;
+* ``kv_cache_append``: one exact entry per case of the reference's kv_cache_append workload file
+  (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18) and one broad gfx950 region.
 
-All gfx950 entries share one evidence id and one pack (``packs/gfx950``).
+Shapes a kernel rejects at launch time (a ValueError) are demoted to the torch fallback by the
+runtime with the reason recorded.  Each operator has its own binding artifact and evidence id; both
+live in one pack (``packs/gfx950``).
 """
 
 from __future__ import annotations
@@ -22,10 +24,16 @@ from typing import Any
 
 OPERATOR = "paged_attention_decode"
 SEMANTIC_VERSION = "1.0"
-PACK_ID = "rk-paged-attention-decode-gfx950"
+PACK_ID = "rk-paged-attention-gfx950"
 PACK_VERSION = "1.0.0"
 EVIDENCE_ID = "mi355x-gfx950-paged_attention_decode-splitk-1"
 ENTRYPOINT = "decode_mfma"
+ARTIFACT = "lib/rk_pa_gfx950.so"
+
+KV_APPEND = "kv_cache_append"
+KV_EVIDENCE_ID = "mi355x-gfx950-kv_cache_append-rowcopy-1"
+KV_ENTRYPOINT = "append"
+KV_ARTIFACT = "lib/rk_kv_gfx950.so"
 
 _INT_MAX = 2**31 - 1
 _POW2_BLOCKS = [1, 2, 4, 8, 16, 32, 64, 128, 256]
@@ -85,53 +93,89 @@ _COMMON = {
 }
 
 
-def _winner(artifact: str, sha256: str) -> dict[str, Any]:
-    return {"provider": "native", "artifact": artifact, "entrypoint": ENTRYPOINT, "sha256": sha256,
+# kv_cache_append: (id suffix, workload constraints).  The reference's cases, each for both dtypes.
+KV_EXACT_REGIONS: list[tuple[str, dict[str, Any]]] = [
+    ("decode-t1-gqa8-d128-p16", {"tokens": 1, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 128}),
+    ("decode-t8-gqa8-d128-p16", {"tokens": 8, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 128}),
+    ("decode-t32-gqa8-d128-p16", {"tokens": 32, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 128}),
+    ("prefill-t128-gqa8-d128-p16", {"tokens": 128, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 128}),
+    ("decode-t32-gqa8-d256-p16", {"tokens": 32, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 256}),
+    ("prefill-t128-mha32-d128-p32", {"tokens": 128, "num_blocks": 128, "block_size": 32, "kv_heads": 32, "head_dim": 128}),
+]
+KV_BROAD_REGION: dict[str, Any] = {
+    "tokens": [1, _INT_MAX],
+    "num_blocks": [1, _INT_MAX],
+    "block_size": [1, _INT_MAX],
+    "kv_heads": [1, 1 << 20],
+    "head_dim": {"one_of": [64, 128, 256]},
+}
+_KV_COMMON = {
+    "dtype": {"one_of": ["fp16", "bf16"]},
+    "index_dtype": {"one_of": ["int32", "int64"]},
+    "layout": "block_slot_head_dim",
+    "contiguous": True,
+    "requires_grad": False,
+}
+
+
+def _winner(artifact: str, entrypoint: str, sha256: str) -> dict[str, Any]:
+    return {"provider": "native", "artifact": artifact, "entrypoint": entrypoint, "sha256": sha256,
             "format": "python_extension"}
 
 
-def render_dispatch_manifest(*, environment: dict[str, Any], artifact: str, sha256: str) -> dict[str, Any]:
-    entries = []
-    for suffix, region, launch in EXACT_REGIONS:
-        entries.append({
-            "id": f"{OPERATOR}-gfx950-{suffix}",
-            "priority": 100,
-            "environment": dict(environment),
-            "workload": {**region, **_COMMON},
-            "winner": _winner(artifact, sha256),
-            "launch": dict(launch),
-            "fallbacks": ["torch"],
-            "evidence_id": EVIDENCE_ID,
-        })
-    entries.append({
-        "id": f"{OPERATOR}-gfx950-region",
-        "priority": 10,
+def _entry(operator: str, suffix: str, priority: int, environment: dict[str, Any], workload: dict[str, Any],
+           winner: dict[str, Any], launch: dict[str, Any], evidence_id: str) -> dict[str, Any]:
+    return {
+        "id": f"{operator}-gfx950-{suffix}",
+        "priority": priority,
         "environment": dict(environment),
-        "workload": {**BROAD_REGION, **_COMMON},
-        "winner": _winner(artifact, sha256),
-        "launch": dict(BROAD_LAUNCH),
+        "workload": workload,
+        "winner": winner,
+        "launch": dict(launch),
         "fallbacks": ["torch"],
-        "evidence_id": EVIDENCE_ID,
-    })
+        "evidence_id": evidence_id,
+    }
+
+
+def render_dispatch_manifest(operator: str, *, environment: dict[str, Any], sha256: str) -> dict[str, Any]:
+    """The dispatch manifest of ``operator``; ``sha256`` is the digest of its binding artifact."""
+
+    if operator == OPERATOR:
+        winner = _winner(ARTIFACT, ENTRYPOINT, sha256)
+        entries = [_entry(OPERATOR, suffix, 100, environment, {**region, **_COMMON}, winner, launch, EVIDENCE_ID)
+                   for suffix, region, launch in EXACT_REGIONS]
+        entries.append(_entry(OPERATOR, "region", 10, environment, {**BROAD_REGION, **_COMMON}, winner,
+                              BROAD_LAUNCH, EVIDENCE_ID))
+    elif operator == KV_APPEND:
+        winner = _winner(KV_ARTIFACT, KV_ENTRYPOINT, sha256)
+        entries = [_entry(KV_APPEND, suffix, 100, environment, {**region, **_KV_COMMON}, winner, {}, KV_EVIDENCE_ID)
+                   for suffix, region in KV_EXACT_REGIONS]
+        entries.append(_entry(KV_APPEND, "region", 10, environment, {**KV_BROAD_REGION, **_KV_COMMON}, winner, {},
+                              KV_EVIDENCE_ID))
+    else:
+        raise KeyError(operator)
     return {
         "schema_version": "1.0",
-        "operator": OPERATOR,
+        "operator": operator,
         "semantic_version": SEMANTIC_VERSION,
         "default_fallbacks": ["torch"],
         "entries": entries,
     }
 
 
-def render_pack_manifest(*, environment: dict[str, Any], artifact: str, sha256: str) -> dict[str, Any]:
+def render_pack_manifest(*, environment: dict[str, Any], digests: dict[str, str]) -> dict[str, Any]:
+    """The pack manifest; ``digests`` maps each operator to its binding artifact's SHA-256."""
+
+    artifacts = [
+        {"operator": OPERATOR, "semantic_version": SEMANTIC_VERSION,
+         **_winner(ARTIFACT, ENTRYPOINT, digests[OPERATOR]), "evidence_id": EVIDENCE_ID},
+        {"operator": KV_APPEND, "semantic_version": SEMANTIC_VERSION,
+         **_winner(KV_ARTIFACT, KV_ENTRYPOINT, digests[KV_APPEND]), "evidence_id": KV_EVIDENCE_ID},
+    ]
     return {
         "schema_version": "1.0",
         "pack_id": PACK_ID,
         "pack_version": PACK_VERSION,
         "environment": dict(environment),
-        "artifacts": [{
-            "operator": OPERATOR,
-            "semantic_version": SEMANTIC_VERSION,
-            **_winner(artifact, sha256),
-            "evidence_id": EVIDENCE_ID,
-        }],
+        "artifacts": artifacts,
     }

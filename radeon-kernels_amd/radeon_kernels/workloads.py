@@ -158,3 +158,68 @@ def aux_bytes(workload: Workload, contexts: list[int], index_size: int = 4) -> i
     cap = workload.max_blocks * workload.block_size
     table = sum(math.ceil(min(max(int(c), 0), cap) / workload.block_size) for c in contexts) * index_size
     return qo + table + workload.batch * index_size
+
+
+# ---------------------------------------------------------------------------------------------
+# Paged KV-cache append: the cases of the reference's workload file
+# (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18), each in fp16 and bf16.
+@dataclass(frozen=True)
+class AppendCase:
+    key: str
+    tokens: int
+    num_blocks: int
+    block_size: int
+    kv_heads: int
+    head_dim: int
+
+    def row_elements(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    def bytes_moved(self, elem_size: int = 2) -> int:
+        """Algorithmic bytes of one append: read K and V rows, write K and V rows."""
+
+        return 4 * self.tokens * self.row_elements() * elem_size
+
+
+APPEND_CASES: dict[str, AppendCase] = {
+    case.key: case
+    for case in (
+        AppendCase("decode-t1-gqa8-d128-p16", 1, 256, 16, 8, 128),
+        AppendCase("decode-t8-gqa8-d128-p16", 8, 256, 16, 8, 128),
+        AppendCase("decode-t32-gqa8-d128-p16", 32, 256, 16, 8, 128),
+        AppendCase("prefill-t128-gqa8-d128-p16", 128, 256, 16, 8, 128),
+        AppendCase("decode-t32-gqa8-d256-p16", 32, 256, 16, 8, 256),
+        AppendCase("prefill-t128-mha32-d128-p32", 128, 128, 32, 32, 128),
+    )
+}
+APPEND_SEED = 20261301
+
+
+def make_append_inputs(case: AppendCase | str, *, dtype: str = "bf16", index_dtype: str = "int64",
+                       seed: int = APPEND_SEED, device: Any = "cpu") -> dict[str, Any]:
+    """Seeded inputs of one append case, generated on the CPU and moved to ``device``.
+
+    Draw order: key cache, value cache, key, value (uniform in [-0.5, 0.5), as the reference's
+    benchmark draws them, benchmarks/kv_cache/benchmark.py:77-80), then the slots: the first
+    ``tokens`` entries of a permutation of all ``num_blocks * block_size`` slots (unique, in range;
+    benchmark.py:100-106).
+    """
+
+    import torch
+
+    if isinstance(case, str):
+        case = APPEND_CASES[case]
+    gen = torch.Generator().manual_seed(seed)
+    t_dtype = torch_dtype(torch, dtype)
+    cache_shape = (case.num_blocks, case.block_size, case.kv_heads, case.head_dim)
+    token_shape = (case.tokens, case.kv_heads, case.head_dim)
+
+    def uniform(shape):
+        return (torch.rand(shape, generator=gen, dtype=torch.float32) - 0.5).to(t_dtype)
+
+    key_cache, value_cache = uniform(cache_shape), uniform(cache_shape)
+    key, value = uniform(token_shape), uniform(token_shape)
+    slots = torch.randperm(case.num_blocks * case.block_size, generator=gen)[: case.tokens]
+    slots = slots.to(torch.int64 if index_dtype == "int64" else torch.int32).contiguous()
+    out = {"key": key, "value": value, "key_cache": key_cache, "value_cache": value_cache, "slot_mapping": slots}
+    return {name: tensor.to(device) for name, tensor in out.items()} | {"case": case, "seed": seed}

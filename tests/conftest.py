@@ -38,3 +38,10 @@ def palib(gpu):
     from radeon_kernels.cabi import library
 
     return library()
+
+
+@pytest.fixture(scope="session")
+def kvlib(gpu):
+    from radeon_kernels.cabi import kv_library
+
+    return kv_library()

@@ -11,10 +11,10 @@ Writes:
                    boundaries 1, block_size, block_size+1.
   c1_expected.npz  the 1-sequence 32/8-head d128 fp16 workload: SHA-256 of each seeded input
                    tensor, float64 brute-force output and its fp16 rounding.
-  reference_dispatch_paged_attention_decode-1.0.json
-                   the reference's published paged-attention dispatch manifest (data, Apache-2.0),
-                   used to prove the gfx950 entries merge into it; copied from /root/reference when
-                   that tree is present.
+  reference_dispatch_paged_attention_decode-1.0.json, reference_dispatch_kv_cache_append-1.0.json
+                   the reference's published dispatch manifests for these operators (data,
+                   Apache-2.0), used to prove the gfx950 entries merge into them; copied from
+                   /root/reference when that tree is present.
 
 The reference repository holds no numeric vectors for this operator; these are produced by the
 oracle's brute force, which the tests pin independently (closed forms, library SDPA, invariants).
@@ -106,11 +106,12 @@ def main() -> None:
         expected_fp16=pa_oracle.round_to_fp16(expected.astype(np.float32)),
     )
 
-    source = Path("/root/reference/dispatch/paged_attention_decode-1.0.json")
-    if source.is_file():
-        document = json.loads(source.read_text(encoding="utf-8"))
-        (HERE / "reference_dispatch_paged_attention_decode-1.0.json").write_text(
-            json.dumps(document, indent=1, sort_keys=True) + "\n", encoding="utf-8")
+    for operator in ("paged_attention_decode", "kv_cache_append"):
+        source = Path(f"/root/reference/dispatch/{operator}-1.0.json")
+        if source.is_file():
+            document = json.loads(source.read_text(encoding="utf-8"))
+            (HERE / f"reference_dispatch_{operator}-1.0.json").write_text(
+                json.dumps(document, indent=1, sort_keys=True) + "\n", encoding="utf-8")
     print("fixtures written to", HERE)
 
 

@@ -157,3 +157,62 @@ def test_workspace_null_pointer_rejected(lib):
     out = ctypes.c_size_t(0)
     assert lib.lib.rk_pa_decode_workspace_bytes(1, 8, 128, 16, 4, 64, None) == cabi.RK_ERR_INVALID_ARGUMENT
     assert lib.lib.rk_pa_decode_workspace_bytes(1, 8, 128, 16, 4, 64, ctypes.byref(out)) == cabi.RK_OK
+
+
+# ---------------------------------------------------------------------------------------------
+# Paged KV-cache library (include/rk_kv_cache.h).
+KV_HEADER = ROOT / "include" / "rk_kv_cache.h"
+
+
+@pytest.fixture(scope="module")
+def kvlib():
+    if not cabi.KV_LIBRARY_PATH.is_file():
+        pytest.fail(f"{cabi.KV_LIBRARY_PATH} is not built; run __graft_entry__.build()")
+    return cabi.KvCacheLibrary()
+
+
+def test_kv_header_and_library_agree(kvlib):
+    text = KV_HEADER.read_text()
+    declared = sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(rk_\w+)\s*\(", text, flags=re.MULTILINE)))
+    assert declared == sorted(cabi.KV_EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(kvlib.lib, name), name
+    for name in ("RK_KV_OK", "RK_KV_ERR_INVALID_ARGUMENT", "RK_KV_ERR_UNSUPPORTED", "RK_KV_ERR_LAUNCH"):
+        assert getattr(cabi, name) == int(re.search(rf"#define {name} (\d+)", text).group(1)), name
+    # Element-type codes are shared with the decode library.
+    assert int(re.search(r"#define RK_KV_DTYPE_BF16 (\d+)", text).group(1)) == cabi.RK_DTYPE_BF16
+    assert int(re.search(r"#define RK_KV_INDEX_INT64 (\d+)", text).group(1)) == cabi.RK_INDEX_INT64
+    assert kvlib.version() == "rk_kv_gfx950 1.0.0 (gfx950, wave64)"
+
+
+def kv_call(lib, **overrides):
+    args = dict(key=16, value=32, key_cache=48, value_cache=64, slot_mapping=80, tokens=4, kv_heads=8, head_dim=128,
+                num_blocks=16, block_size=16, dtype=cabi.RK_DTYPE_BF16, index_dtype=cabi.RK_INDEX_INT64, stream=0)
+    args.update(overrides)
+    return lib.append_raw(**args), lib.last_error()
+
+
+@pytest.mark.parametrize(
+    "overrides, status, message",
+    [
+        (dict(key=0), cabi.RK_KV_ERR_INVALID_ARGUMENT, "must not be NULL"),
+        (dict(slot_mapping=0), cabi.RK_KV_ERR_INVALID_ARGUMENT, "must not be NULL"),
+        (dict(dtype=5), cabi.RK_KV_ERR_INVALID_ARGUMENT, "dtype"),
+        (dict(index_dtype=2), cabi.RK_KV_ERR_INVALID_ARGUMENT, "index_dtype"),
+        (dict(tokens=0), cabi.RK_KV_ERR_INVALID_ARGUMENT, "positive"),
+        (dict(block_size=-1), cabi.RK_KV_ERR_INVALID_ARGUMENT, "positive"),
+        (dict(value=40), cabi.RK_KV_ERR_UNSUPPORTED, "16-byte aligned"),
+        (dict(kv_heads=1, head_dim=7), cabi.RK_KV_ERR_UNSUPPORTED, "multiple of 16 bytes"),
+        (dict(tokens=1 << 24, kv_heads=32, head_dim=128), cabi.RK_KV_ERR_UNSUPPORTED, "index range"),
+    ],
+)
+@cpu_only
+def test_kv_invalid_arguments_are_rejected_before_launch(kvlib, overrides, status, message):
+    got, text = kv_call(kvlib, **overrides)
+    assert got == status, text
+    assert message in text
+
+
+def test_kv_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(FileNotFoundError, match="build"):
+        cabi.KvCacheLibrary(tmp_path / "absent.so")

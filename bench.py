@@ -20,8 +20,8 @@ Prints one JSON line:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5] [--variant mfma]
                        [--partition P] [--no-cpu-baseline] [--cpu-seconds S] [--calibration-copy]
-       python bench.py --operator kv_cache_append [--case prefill-t128-mha32-d128-p32] [--dtype bf16]
-                       (the paged-cache writer that feeds the decode; same JSON line shape)
+       python bench.py --operator kv_cache_append|kv_cache_copy [--case ...] [--dtype bf16]
+                       (the paged-cache operators around the decode; same JSON line shape)
 """
 
 from __future__ import annotations
@@ -57,11 +57,30 @@ def parse_args(argv=None):
     parser.add_argument("--calibration-copy", action="store_true",
                         help="run a 1 GiB device copy before timing (counter calibration under rocprofv3)")
     parser.add_argument("--operator", default="paged_attention_decode",
-                        choices=["paged_attention_decode", "kv_cache_append"])
-    parser.add_argument("--case", default="prefill-t128-mha32-d128-p32",
-                        help="kv_cache_append case (benchmarks/workloads/kv_cache_append-1.0.yaml in the reference)")
-    parser.add_argument("--dtype", default="bf16", choices=["fp16", "bf16"], help="kv_cache_append element type")
+                        choices=["paged_attention_decode", "kv_cache_append", "kv_cache_copy"])
+    parser.add_argument("--case", default=None,
+                        help="kv_cache_append / kv_cache_copy case (benchmarks/workloads/kv_cache_*-1.0.yaml in the "
+                             "reference); defaults: prefill-t128-mha32-d128-p32, beam-pairs64-gqa8-d256-p16")
+    parser.add_argument("--dtype", default="bf16", choices=["fp16", "bf16"], help="KV-cache operator element type")
     return parser.parse_args(argv)
+
+
+def public_call_us(torch, call, steps: int, batches: int = 5) -> float:
+    """Host wall time per call of the public operator: the median of ``batches`` batches of ``steps``
+    back-to-back calls, each batch closed by a synchronisation (single batches were seen to catch
+    one-off host stalls of the box)."""
+
+    import statistics
+
+    times = []
+    for _ in range(batches):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(steps):
+            call()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t) / steps * 1e6)
+    return statistics.median(times)
 
 
 def dispatch_launch(workload_key: str) -> tuple[str, int]:
@@ -141,37 +160,47 @@ def cpu_baseline(torch, data, seconds: float) -> dict:
     }
 
 
-def main_append(args) -> int:
-    """``--operator kv_cache_append``: one step = one append of the case's tokens (one kernel)."""
+def main_kv(args) -> int:
+    """``--operator kv_cache_append|kv_cache_copy``: one step = one call of the case (one kernel)."""
 
     import torch
 
     from radeon_kernels.cabi import kv_library
-    from radeon_kernels.workloads import APPEND_CASES, make_append_inputs
+    from radeon_kernels.workloads import APPEND_CASES, COPY_CASES, make_append_inputs, make_copy_inputs
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no visible ROCm GPU"}))
         return 1
     device = torch.device("cuda:0")
     lib = kv_library()  # raises if the HIP library was not built
-    case = APPEND_CASES[args.case]
-    data = make_append_inputs(case, dtype=args.dtype, index_dtype="int64", device=device)
-    moved = case.bytes_moved() + case.tokens * 8  # K/V rows read and written, plus the slots
+    if args.operator == "kv_cache_append":
+        case = APPEND_CASES[args.case or "prefill-t128-mha32-d128-p32"]
+        data = make_append_inputs(case, dtype=args.dtype, index_dtype="int64", device=device)
+        names = ("key", "value", "key_cache", "value_cache", "slot_mapping")
+        moved = case.bytes_moved() + case.tokens * 8  # K/V rows read and written, plus the slots
+        launch, kernel = lib.append, "kv_append_kernel"
+        shape = {"tokens": case.tokens}
+    else:
+        case = COPY_CASES[args.case or "beam-pairs64-gqa8-d256-p16"]
+        data = make_copy_inputs(case, dtype=args.dtype, index_dtype="int64", device=device)
+        names = ("key_cache", "value_cache", "block_mapping")
+        moved = case.bytes_moved() + case.pairs * 16  # K/V blocks read and written, plus the mapping
+        launch, kernel = lib.copy, "kv_copy_kernel"
+        shape = {"pairs": case.pairs}
     cache_bytes = data["key_cache"].numel() * 2 * 2
     # The caches fit in the 256 MB last-level cache: rotate among enough independent copies of every
     # input that each call's rows come from and go to HBM.
     copies = max(16, math.ceil(768e6 / cache_bytes))
-    names = ("key", "value", "key_cache", "value_cache", "slot_mapping")
     sets = [tuple(data[n] for n in names)] + [tuple(data[n].clone() for n in names) for _ in range(copies - 1)]
     stream = torch.cuda.current_stream(device)
     for i in range(args.warmup):
-        lib.append(*sets[i % copies], stream=stream)
+        launch(*sets[i % copies], stream=stream)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t = time.perf_counter()
     start.record(stream)
     for i in range(args.steps):
-        lib.append(*sets[i % copies], stream=stream)
+        launch(*sets[i % copies], stream=stream)
     end.record(stream)
     torch.cuda.synchronize()
     us_per_call = (time.perf_counter() - t) / args.steps * 1e6
@@ -179,7 +208,7 @@ def main_append(args) -> int:
     torch.cuda.synchronize()
     t = time.perf_counter()
     for _ in range(args.steps):
-        lib.append(*sets[0], stream=stream)
+        launch(*sets[0], stream=stream)
     torch.cuda.synchronize()
     hot = (time.perf_counter() - t) / args.steps * 1e6
 
@@ -188,19 +217,15 @@ def main_append(args) -> int:
     import radeon_kernels as rk
     from radeon_kernels.ops._runtime import NativeDemotionWarning
 
+    public = rk.kv_cache_append if args.operator == "kv_cache_append" else rk.kv_cache_copy
     with warnings.catch_warnings():
         warnings.simplefilter("error", NativeDemotionWarning)
-        rk.kv_cache_append(*sets[0])
+        public(*sets[0])
     decision = rk.get_last_dispatch()
-    torch.cuda.synchronize()
-    t = time.perf_counter()
-    for _ in range(args.steps):
-        rk.kv_cache_append(*sets[0])
-    torch.cuda.synchronize()
-    rk_us = (time.perf_counter() - t) / args.steps * 1e6
+    rk_us = public_call_us(torch, lambda: public(*sets[0]), max(1, args.steps // 5))
 
     result = {
-        "metric": "kv_cache_append µs/call + effective GB/s (% MI355X HBM peak)",
+        "metric": f"{args.operator} µs/call + effective GB/s (% MI355X HBM peak)",
         "value": round(moved / (us_per_call * 1e3), 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -211,17 +236,17 @@ def main_append(args) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.dtype,
-        "data": "synthetic (seeded uniform[-0.5, 0.5) K/V and caches, unique random slots)",
+        "data": "synthetic (seeded uniform[-0.5, 0.5) values, unique random slots / disjoint block pairs)",
         "config": {
-            "workload": f"kv_cache_append-{case.key}-{args.dtype}", "tokens": case.tokens,
-            "num_blocks": case.num_blocks, "block_size": case.block_size, "kv_heads": case.kv_heads,
-            "head_dim": case.head_dim, "index_dtype": "int64", "copies_rotated": copies, "arch":
-            torch.cuda.get_device_properties(0).gcnArchName.split(":", 1)[0],
+            "workload": f"{args.operator}-{case.key}-{args.dtype}", **shape, "num_blocks": case.num_blocks,
+            "block_size": case.block_size, "kv_heads": case.kv_heads, "head_dim": case.head_dim,
+            "index_dtype": "int64", "copies_rotated": copies,
+            "arch": torch.cuda.get_device_properties(0).gcnArchName.split(":", 1)[0],
         },
         "us_per_call": round(us_per_call, 2),
         "us_per_call_cache_resident": round(hot, 2),
         "bytes_per_call": moved,
-        "kernels_us": {"kv_append_kernel": round(kernel_us, 2)},
+        "kernels_us": {kernel: round(kernel_us, 2)},
         "roofline": {
             "bound": "hbm",
             "achieved": round(moved / (kernel_us * 1e3), 1),
@@ -231,35 +256,39 @@ def main_append(args) -> int:
             "traffic": None,
         },
         "rk_call": {"us_per_call": round(rk_us, 2), "selected": decision["selected"], "entry_id": decision["entry_id"]},
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_append(torch, data, min(args.cpu_seconds, 5.0)),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_kv(torch, args.operator, data, moved,
+                                                                           min(args.cpu_seconds, 5.0)),
     }
     print(json.dumps(result), flush=True)
     return 0
 
 
-def cpu_baseline_append(torch, data, seconds: float) -> dict:
-    """The reference fallback's steps (index_copy_ into the slot view) on CPU copies of the inputs."""
+def cpu_baseline_kv(torch, operator: str, data, moved: int, seconds: float) -> dict:
+    """The reference fallback's steps (index_select / index_copy_) on CPU copies of the inputs."""
 
     from oracle import kv_oracle
 
     threads = torch.get_num_threads()
-    case = data["case"]
-    cpu = {n: data[n].cpu() for n in ("key", "value", "key_cache", "value_cache", "slot_mapping")}
+    if operator == "kv_cache_append":
+        cpu = [data[n].cpu() for n in ("key", "value", "key_cache", "value_cache", "slot_mapping")]
+        step = lambda: kv_oracle.append_inplace_torch(torch, *cpu)  # noqa: E731
+    else:
+        cpu = [data[n].cpu() for n in ("key_cache", "value_cache", "block_mapping")]
+        step = lambda: kv_oracle.copy_inplace_torch(torch, *cpu)  # noqa: E731
     calls, elapsed = 0, 0.0
     while elapsed < seconds:
         t = time.perf_counter()
-        for _ in range(100):
-            kv_oracle.append_inplace_torch(torch, cpu["key"], cpu["value"], cpu["key_cache"], cpu["value_cache"],
-                                           cpu["slot_mapping"])
+        for _ in range(20):
+            step()
         elapsed += time.perf_counter() - t
-        calls += 100
+        calls += 20
     us = elapsed / calls * 1e6
     return {
-        "value": round((case.bytes_moved() + case.tokens * 8) / (us * 1e3), 3),
+        "value": round(moved / (us * 1e3), 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{calls} appends of the same case on CPU tensors by the reference fallback's index_copy_ steps "
+        "sample": (f"{calls} calls of the same case on CPU tensors by the reference fallback's torch steps "
                    f"(oracle/kv_oracle.py; torch {torch.__version__}, {threads} threads), {elapsed:.1f} s"),
         "us_per_call": round(us, 2),
     }
@@ -267,8 +296,8 @@ def cpu_baseline_append(torch, data, seconds: float) -> dict:
 
 def main(argv=None) -> int:
     args = parse_args(argv)
-    if args.gpus == 1 and args.operator == "kv_cache_append":
-        return main_append(args)
+    if args.gpus == 1 and args.operator != "paged_attention_decode":
+        return main_kv(args)
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only; the decode shards by sequence and KV head "
                           "with no exchange, so multi-GPU throughput is N x the single-GPU value and is not measured here",
@@ -376,12 +405,7 @@ def main(argv=None) -> int:
         warnings.simplefilter("error", NativeDemotionWarning)
         rk.paged_attention_decode(q, k, v, bt, cl)
     decision = rk.get_last_dispatch()
-    torch.cuda.synchronize()
-    t = time.perf_counter()
-    for _ in range(args.steps):
-        rk.paged_attention_decode(q, k, v, bt, cl)
-    torch.cuda.synchronize()
-    rk_us = (time.perf_counter() - t) / args.steps * 1e6
+    rk_us = public_call_us(torch, lambda: rk.paged_attention_decode(q, k, v, bt, cl), max(1, args.steps // 5))
 
     traffic = read_traffic(w.name, variant, partition)
     result = {

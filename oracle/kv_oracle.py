@@ -1,4 +1,4 @@
-"""CPU oracle for the paged KV-cache append -- TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for the paged KV-cache append and block copy -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/`` and the ``cpu_baseline`` leg of ``bench.py`` may import this module, and only as
 the checker (or the timed CPU baseline).  The product path (``radeon_kernels``) never imports it.
@@ -12,9 +12,14 @@ written to slot ``slot_mapping[t]`` (block ``slot // block_size``, offset ``slot
 
 Both skip a slot outside ``[0, num_blocks * block_size)`` instead of raising as ``index_copy_``
 does: that is the native kernel's documented behaviour (the reference's own kernel does the same,
-benchmarks/kv_cache/native_kv_cache.hip:42-45), and the contract requires in-range slots anyway
+benchmarks/kv_cache/native_kv_cache.hip:44-46), and the contract requires in-range slots anyway
 (contracts/kv_cache_append-1.0.json:19).  With duplicate slots (outside the contract) the last
 token wins here; the kernel gives no order guarantee.
+
+``copy_numpy`` restates the block copy (reference.py:23-38): a snapshot of every source block is
+taken first, then written to its destination, so overlapping mappings (outside the contract) still
+read pre-call contents; a pair with a block id outside ``[0, num_blocks)`` is skipped, as the
+native kernels do (native_kv_cache.hip:72-74).
 
 Pinning (``tests/test_kv_oracle.py``): against torch's ``index_copy_`` on every reference case,
 against the brute force on small shapes, and by invariants (untouched slots unchanged, gathering
@@ -79,3 +84,29 @@ def append_inplace_torch(torch: Any, key: Any, value: Any, key_cache: Any, value
     rows = (-1, int(key_cache.shape[2]), int(key_cache.shape[3]))
     key_cache.view(rows).index_copy_(0, slots, key)
     value_cache.view(rows).index_copy_(0, slots, value)
+
+
+def copy_numpy(key_cache: np.ndarray, value_cache: np.ndarray, block_mapping: Any) -> tuple[np.ndarray, np.ndarray]:
+    """New (key_cache, value_cache) arrays with each source block copied to its destination block."""
+
+    num_blocks = key_cache.shape[0]
+    pairs = [(int(s), int(d)) for s, d in np.asarray(block_mapping, dtype=np.int64).tolist()]
+    pairs = [(s, d) for s, d in pairs if 0 <= s < num_blocks and 0 <= d < num_blocks]
+    k_out, v_out = key_cache.copy(), value_cache.copy()
+    k_snap = [key_cache[s].copy() for s, _ in pairs]
+    v_snap = [value_cache[s].copy() for s, _ in pairs]
+    for (_, d), k_block, v_block in zip(pairs, k_snap, v_snap):
+        k_out[d] = k_block
+        v_out[d] = v_block
+    return k_out, v_out
+
+
+def copy_inplace_torch(torch: Any, key_cache: Any, value_cache: Any, block_mapping: Any) -> None:
+    """The reference fallback's own steps (reference.py:30-37) on CPU tensors, in place: the CPU path
+    the gfx950 copy kernel is timed beside."""
+
+    mapping = block_mapping.to(dtype=torch.int64)
+    k = key_cache.index_select(0, mapping[:, 0])
+    v = value_cache.index_select(0, mapping[:, 0])
+    key_cache.index_copy_(0, mapping[:, 1], k)
+    value_cache.index_copy_(0, mapping[:, 1], v)

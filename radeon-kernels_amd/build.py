@@ -5,7 +5,8 @@ Outputs (all under ``radeon-kernels_amd/packs/gfx950``):
 * ``lib/librk_pa_gfx950.so`` -- paged-attention decode C-ABI library (``include/rk_paged_attention.h``).
 * ``lib/rk_pa_gfx950.so``    -- its PyTorch-ROCm binding (module ``rk_pa_gfx950``).
 * ``lib/librk_kv_gfx950.so`` -- paged KV-cache C-ABI library (``include/rk_kv_cache.h``).
-* ``lib/rk_kv_gfx950.so``    -- its PyTorch-ROCm binding (module ``rk_kv_gfx950``).
+* ``lib/rk_kv_append_gfx950.so``, ``lib/rk_kv_copy_gfx950.so`` -- its PyTorch-ROCm bindings, one
+  module per operator (a pack names one artifact file per operator), built from one source.
 * ``manifest.json``          -- the kernel-pack manifest (same fields as the reference's
   ``schemas/kernel-pack.schema.json``), stamped with the bindings' SHA-256 and this environment.
 
@@ -107,23 +108,26 @@ def sha256_file(path: Path) -> str:
 
 
 class Library:
-    """One C-ABI kernel library (hipcc) plus the torch binding (g++) that links against it."""
+    """One C-ABI kernel library (hipcc) plus the torch binding modules (g++) that link against it.
 
-    def __init__(self, operator: str, hip_source: str, cabi_name: str, binding_source: str, module: str,
-                 digest_symbol: str) -> None:
-        self.operator = operator
+    ``bindings`` maps each binding module name to the operators whose dispatch entries name it; a
+    pack needs one artifact file per operator, so operators sharing a library get one module each,
+    all built from the same binding source."""
+
+    def __init__(self, hip_source: str, cabi_name: str, binding_source: str, digest_symbol: str,
+                 bindings: dict[str, tuple[str, ...]]) -> None:
         self.hip_source = CSRC / hip_source
         self.cabi_name = cabi_name
         self.binding_source = CSRC / binding_source
-        self.module = module
         self.digest_symbol = digest_symbol
+        self.bindings = bindings
 
 
 LIBRARIES = (
-    Library("paged_attention_decode", "pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", EXTENSION_NAME,
-            "kRkKernelLibrarySha256"),
-    Library("kv_cache_append", "kv_cache_gfx950.hip", "librk_kv_gfx950.so", "kv_torch_ext.cpp", "rk_kv_gfx950",
-            "kRkKvLibrarySha256"),
+    Library("pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", "kRkKernelLibrarySha256",
+            {EXTENSION_NAME: ("paged_attention_decode",)}),
+    Library("kv_cache_gfx950.hip", "librk_kv_gfx950.so", "kv_torch_ext.cpp", "kRkKvLibrarySha256",
+            {"rk_kv_append_gfx950": ("kv_cache_append",), "rk_kv_copy_gfx950": ("kv_cache_copy",)}),
 )
 
 
@@ -145,64 +149,72 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
     for lib in LIBRARIES:
         cabi_tmp = work / lib.cabi_name
         hip = _run([_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(lib.hip_source), "-o", str(cabi_tmp)], verbose)
-        ext_obj = work / f"{lib.module}.o"
-        cxx = [
-            "g++",
-            "-O2",
-            "-std=c++17",
-            "-fPIC",
-            "-c",
-            "-D__HIP_PLATFORM_AMD__=1",
-            "-DUSE_ROCM=1",
-            f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
-            f"-DTORCH_EXTENSION_NAME={lib.module}",
-            "-DTORCH_API_INCLUDE_EXTENSION_H",
-            f"-ffile-prefix-map={REPO_ROOT}=.",
-            *[f"-I{path}" for path in includes],
-            f"-I{sysconfig.get_paths()['include']}",
-            f"-I{INCLUDE}",
-            str(lib.binding_source),
-            "-o",
-            str(ext_obj),
-        ]
-        jobs.append((lib, cabi_tmp, ext_obj, hip, _run(cxx, verbose)))
+        objects = {}
+        for module in lib.bindings:
+            ext_obj = work / f"{module}.o"
+            cxx = [
+                "g++",
+                "-O2",
+                "-std=c++17",
+                "-fPIC",
+                "-c",
+                "-D__HIP_PLATFORM_AMD__=1",
+                "-DUSE_ROCM=1",
+                f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+                f"-DTORCH_EXTENSION_NAME={module}",
+                "-DTORCH_API_INCLUDE_EXTENSION_H",
+                f"-ffile-prefix-map={REPO_ROOT}=.",
+                *[f"-I{path}" for path in includes],
+                f"-I{sysconfig.get_paths()['include']}",
+                f"-I{INCLUDE}",
+                str(lib.binding_source),
+                "-o",
+                str(ext_obj),
+            ]
+            objects[module] = (ext_obj, _run(cxx, verbose))
+        jobs.append((lib, cabi_tmp, hip, objects))
 
     bindings: dict[str, Path] = {}
-    for lib, cabi_tmp, ext_obj, hip, gxx in jobs:
+    for lib, cabi_tmp, hip, objects in jobs:
         _finish(hip, f"hipcc ({lib.cabi_name})")
-        # The binding checks at import that the kernel library it loads is the one built here.
-        digest_src = work / f"{lib.module}_digest.cpp"
-        digest_obj = work / f"{lib.module}_digest.o"
+        # The bindings check at import that the kernel library they load is the one built here.
+        digest_src = work / f"{lib.cabi_name}.digest.cpp"
+        digest_obj = work / f"{lib.cabi_name}.digest.o"
         digest_src.write_text(f'extern const char {lib.digest_symbol}[] = "{sha256_file(cabi_tmp)}";\n')
         _finish(_run(["g++", "-O2", "-fPIC", "-c", str(digest_src), "-o", str(digest_obj)], verbose),
-                f"g++ ({lib.module} library digest)")
-        _finish(gxx, f"g++ ({lib.module} binding)")
-        ext_tmp = work / f"{lib.module}.so"
-        link = [
-            "g++",
-            "-shared",
-            str(ext_obj),
-            str(digest_obj),
-            f"-L{work}",
-            *[f"-L{path}" for path in libraries],
-            "-l:" + lib.cabi_name,
-            "-lc10",
-            "-lc10_hip",
-            "-ltorch",
-            "-ltorch_cpu",
-            "-ltorch_hip",
-            "-ltorch_python",
-            "-Wl,-rpath,$ORIGIN",
-            "-Wl,--build-id=none",
-            "-o",
-            str(ext_tmp),
-        ]
-        _finish(_run(link, verbose), f"link ({lib.module} binding)")
+                f"g++ ({lib.cabi_name} digest)")
+        linked = []
+        for module, (ext_obj, gxx) in objects.items():
+            _finish(gxx, f"g++ ({module} binding)")
+            ext_tmp = work / f"{module}.so"
+            link = [
+                "g++",
+                "-shared",
+                str(ext_obj),
+                str(digest_obj),
+                f"-L{work}",
+                *[f"-L{path}" for path in libraries],
+                "-l:" + lib.cabi_name,
+                "-lc10",
+                "-lc10_hip",
+                "-ltorch",
+                "-ltorch_cpu",
+                "-ltorch_hip",
+                "-ltorch_python",
+                "-Wl,-rpath,$ORIGIN",
+                "-Wl,--build-id=none",
+                "-o",
+                str(ext_tmp),
+            ]
+            _finish(_run(link, verbose), f"link ({module} binding)")
+            linked.append((module, ext_obj, ext_tmp))
         os.replace(cabi_tmp, LIB_DIR / lib.cabi_name)
-        os.replace(ext_tmp, LIB_DIR / f"{lib.module}.so")
-        ext_obj.unlink()
+        for module, ext_obj, ext_tmp in linked:
+            os.replace(ext_tmp, LIB_DIR / f"{module}.so")
+            ext_obj.unlink()
+            for operator in lib.bindings[module]:
+                bindings[operator] = LIB_DIR / f"{module}.so"
         digest_obj.unlink()
-        bindings[lib.operator] = LIB_DIR / f"{lib.module}.so"
     return bindings
 
 

@@ -1,10 +1,10 @@
-// Paged KV-cache append for MI355X (gfx950, CDNA4, wave64).
+// Paged KV-cache append and block copy for MI355X (gfx950, CDNA4, wave64).
 //
-// Operator semantics follow the reference fallback (src/radeon_kernels/ops/kv_cache/reference.py:6-20)
+// Append semantics follow the reference fallback (src/radeon_kernels/ops/kv_cache/reference.py:6-20)
 // and contract (contracts/kv_cache_append-1.0.json:15-22): token t's K row and V row, each
 // kv_heads * head_dim contiguous elements, are copied bit for bit to physical slot slot_mapping[t]
 // of the [num_blocks * block_size, kv_heads, head_dim] view of the caches.  A slot outside the
-// cache is skipped, as the reference's own kernel does (benchmarks/kv_cache/native_kv_cache.hip:42-45).
+// cache is skipped, as the reference's own kernel does (benchmarks/kv_cache/native_kv_cache.hip:44-46).
 //
 // A K/V row is the unit both sides share: contiguous in the token tensors and contiguous in the
 // cache (one slot of one block).  So the kernel is a row gather/scatter of 16-byte chunks:
@@ -17,6 +17,18 @@
 //
 // Algorithmic bytes: 4 * tokens * kv_heads * head_dim * 2 (read K and V, write K and V) plus the
 // slot indices; it is an HBM-bound copy with no arithmetic.
+//
+// Copy semantics follow reference.py:23-38 and contracts/kv_cache_copy-1.0.json:14-19: for every pair
+// of block_mapping [pairs, 2], cache block `source` (K and V) is copied to block `destination`, each
+// reading the pre-call contents.  The contract makes destinations unique and disjoint from the
+// sources, so a direct copy has exactly those snapshot semantics.  A pair with either block outside
+// the cache is skipped (native_kv_cache.hip:72-74).
+//
+//   kv_copy_kernel    one workgroup per (pair, 16 KB run of the block): each lane moves four
+//                     16-byte chunks of K and four of V, all eight loads in flight before the stores.
+//                     The two block ids are wave-uniform scalar loads.
+//
+// Algorithmic bytes: 4 * pairs * block_size * kv_heads * head_dim * 2 plus the mapping.
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
@@ -61,6 +73,50 @@ __global__ __launch_bounds__(kMaxThreads) void kv_append_kernel(AppendParams p) 
   const int64_t dst = slot * p.row_chunks + chunk;
   p.key_cache[dst] = k;
   p.value_cache[dst] = v;
+}
+
+constexpr int kCopyUnroll = 4;  // chunks per lane per tensor in the copy kernel
+
+struct CopyParams {
+  u32x4* key_cache;
+  u32x4* value_cache;
+  const void* mapping;   // [pairs, 2] (source, destination)
+  int64_t num_blocks;
+  int64_t block_chunks;  // 16-byte chunks per cache block (block_size * kv_heads * head_dim * 2 / 16)
+  int32_t runs;          // workgroups per block
+  int32_t index_is64;
+};
+
+__global__ __launch_bounds__(kMaxThreads) void kv_copy_kernel(CopyParams p) {
+  const int pair = static_cast<int>(blockIdx.x) / p.runs;
+  const int run = static_cast<int>(blockIdx.x) - pair * p.runs;
+  const int64_t src = p.index_is64 ? static_cast<const int64_t*>(p.mapping)[2 * pair]
+                                   : static_cast<int64_t>(static_cast<const int32_t*>(p.mapping)[2 * pair]);
+  const int64_t dst = p.index_is64 ? static_cast<const int64_t*>(p.mapping)[2 * pair + 1]
+                                   : static_cast<int64_t>(static_cast<const int32_t*>(p.mapping)[2 * pair + 1]);
+  if (src < 0 || dst < 0 || src >= p.num_blocks || dst >= p.num_blocks) return;
+  const int64_t first = static_cast<int64_t>(run) * kCopyUnroll * blockDim.x + threadIdx.x;
+  const u32x4* ks = p.key_cache + src * p.block_chunks;
+  const u32x4* vs = p.value_cache + src * p.block_chunks;
+  u32x4 k[kCopyUnroll], v[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t c = first + static_cast<int64_t>(u) * blockDim.x;
+    if (c < p.block_chunks) {
+      k[u] = ks[c];
+      v[u] = vs[c];
+    }
+  }
+  u32x4* kd = p.key_cache + dst * p.block_chunks;
+  u32x4* vd = p.value_cache + dst * p.block_chunks;
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t c = first + static_cast<int64_t>(u) * blockDim.x;
+    if (c < p.block_chunks) {
+      kd[c] = k[u];
+      vd[c] = v[u];
+    }
+  }
 }
 
 thread_local std::string g_last_error;
@@ -124,6 +180,48 @@ extern "C" int rk_kv_cache_append(const void* key, const void* value, void* key_
   prm.row_blocks = static_cast<int32_t>(row_blocks);
   prm.index_is64 = index_dtype == RK_KV_INDEX_INT64 ? 1 : 0;
   hipLaunchKernelGGL(kv_append_kernel, dim3(static_cast<uint32_t>(grid)),
+                     dim3(static_cast<uint32_t>(threads)), 0, static_cast<hipStream_t>(stream), prm);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(RK_KV_ERR_LAUNCH, "launch failed: %s", hipGetErrorString(err));
+  return RK_KV_OK;
+}
+
+extern "C" int rk_kv_cache_copy(void* key_cache, void* value_cache, const void* block_mapping,
+                                int64_t pairs, int64_t num_blocks, int64_t block_size,
+                                int64_t kv_heads, int64_t head_dim, int dtype, int index_dtype,
+                                void* stream) {
+  if (key_cache == nullptr || value_cache == nullptr || block_mapping == nullptr)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "tensor pointers must not be NULL");
+  if (dtype != RK_KV_DTYPE_FP16 && dtype != RK_KV_DTYPE_BF16)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (index_dtype != RK_KV_INDEX_INT32 && index_dtype != RK_KV_INDEX_INT64)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "unknown index_dtype %d", index_dtype);
+  if (pairs <= 0 || num_blocks <= 0 || block_size <= 0 || kv_heads <= 0 || head_dim <= 0)
+    return fail(RK_KV_ERR_INVALID_ARGUMENT, "tensor dimensions must be positive");
+  if (!aligned16(key_cache) || !aligned16(value_cache))
+    return fail(RK_KV_ERR_UNSUPPORTED, "caches must be 16-byte aligned");
+  if (block_size > (int64_t{1} << 40) / kv_heads / head_dim)
+    return fail(RK_KV_ERR_UNSUPPORTED, "shape exceeds the index range of this kernel");
+  const int64_t block_bytes = block_size * kv_heads * head_dim * 2;
+  if (block_bytes % kChunk != 0)
+    return fail(RK_KV_ERR_UNSUPPORTED, "block_size * kv_heads * head_dim * 2 must be a multiple of 16 bytes");
+  const int64_t block_chunks = block_bytes / kChunk;
+  if (num_blocks > (int64_t{1} << 50) / block_chunks)
+    return fail(RK_KV_ERR_UNSUPPORTED, "shape exceeds the index range of this kernel");
+  const int64_t threads = block_chunks >= kMaxThreads ? kMaxThreads : ((block_chunks + 63) / 64) * 64;
+  const int64_t runs = (block_chunks + threads * kCopyUnroll - 1) / (threads * kCopyUnroll);
+  if (pairs > (int64_t{1} << 30) || pairs * runs >= (int64_t{1} << 31))
+    return fail(RK_KV_ERR_UNSUPPORTED, "launch grid exceeds 2^31 workgroups");
+
+  CopyParams prm{};
+  prm.key_cache = static_cast<u32x4*>(key_cache);
+  prm.value_cache = static_cast<u32x4*>(value_cache);
+  prm.mapping = block_mapping;
+  prm.num_blocks = num_blocks;
+  prm.block_chunks = block_chunks;
+  prm.runs = static_cast<int32_t>(runs);
+  prm.index_is64 = index_dtype == RK_KV_INDEX_INT64 ? 1 : 0;
+  hipLaunchKernelGGL(kv_copy_kernel, dim3(static_cast<uint32_t>(pairs * runs)),
                      dim3(static_cast<uint32_t>(threads)), 0, static_cast<hipStream_t>(stream), prm);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(RK_KV_ERR_LAUNCH, "launch failed: %s", hipGetErrorString(err));

@@ -1,10 +1,12 @@
 // PyTorch-ROCm binding of the gfx950 paged KV-cache library (include/rk_kv_cache.h).
 //
-// The python_extension artifact that kv_cache_append dispatch entries name.  Its entrypoint keeps
-// the calling convention of the reference bindings (benchmarks/kv_cache/native_kv_cache.hip:259-283,
-// invoked by src/radeon_kernels/providers/native.py:25 as entrypoint(key, value, key_cache,
-// value_cache, slot_mapping)): it validates, writes the caches in place on the current HIP stream and
-// returns them.  No host synchronisation, no device-to-host reads: safe under HIP graph capture.
+// The python_extension artifacts that kv_cache_append and kv_cache_copy dispatch entries name (one
+// module per operator, rk_kv_append_gfx950 and rk_kv_copy_gfx950, both built from this file).  Its
+// entrypoints keep the calling convention of the reference bindings
+// (benchmarks/kv_cache/native_kv_cache.hip:259-298, invoked by src/radeon_kernels/providers/native.py:25
+// as append(key, value, key_cache, value_cache, slot_mapping) and copy(key_cache, value_cache,
+// block_mapping)): they validate, write the caches in place on the current HIP stream and return
+// them.  No host synchronisation, no device-to-host reads: safe under HIP graph capture.
 //
 // The kernels live in librk_kv_gfx950.so next to this module.  The build bakes that library's
 // SHA-256 into this module and the import fails unless the library actually loaded has it, so the
@@ -27,7 +29,7 @@ namespace {
 std::string loaded_kernel_library_digest(std::string* path_out) {
   Dl_info info{};
   if (dladdr(reinterpret_cast<void*>(&rk_kv_version), &info) == 0 || info.dli_fname == nullptr) {
-    throw py::import_error("rk_kv_gfx950: cannot locate the loaded kernel library");
+    throw py::import_error("rk_kv: cannot locate the loaded kernel library");
   }
   *path_out = info.dli_fname;
   py::bytes content = py::module_::import("pathlib").attr("Path")(*path_out).attr("read_bytes")();
@@ -73,25 +75,54 @@ std::vector<at::Tensor> append(const at::Tensor& key, const at::Tensor& value, a
       key_cache.size(1), key.scalar_type() == at::kBFloat16 ? RK_KV_DTYPE_BF16 : RK_KV_DTYPE_FP16,
       slot_mapping.scalar_type() == at::kLong ? RK_KV_INDEX_INT64 : RK_KV_INDEX_INT32, stream);
   if (status == RK_KV_ERR_INVALID_ARGUMENT || status == RK_KV_ERR_UNSUPPORTED) {
-    TORCH_CHECK_VALUE(false, "rk_kv_gfx950: ", rk_kv_last_error());
+    TORCH_CHECK_VALUE(false, "rk_kv: ", rk_kv_last_error());
   }
-  TORCH_CHECK(status == RK_KV_OK, "rk_kv_gfx950: ", rk_kv_last_error());
+  TORCH_CHECK(status == RK_KV_OK, "rk_kv: ", rk_kv_last_error());
+  return {key_cache, value_cache};
+}
+
+std::vector<at::Tensor> copy(at::Tensor key_cache, at::Tensor value_cache, const at::Tensor& block_mapping) {
+  check_data(key_cache, "key_cache", 4);
+  check_data(value_cache, "value_cache", 4);
+  TORCH_CHECK_VALUE(block_mapping.is_cuda() && block_mapping.dim() == 2 && block_mapping.is_contiguous(),
+                    "block_mapping must be a contiguous rank-2 ROCm tensor");
+  TORCH_CHECK_TYPE(block_mapping.scalar_type() == at::kInt || block_mapping.scalar_type() == at::kLong,
+                   "block_mapping must use INT32 or INT64");
+  const auto device = key_cache.device();
+  TORCH_CHECK_VALUE(value_cache.device() == device && block_mapping.device() == device,
+                    "all tensors must be on the key_cache device");
+  TORCH_CHECK_TYPE(value_cache.scalar_type() == key_cache.scalar_type(), "cache dtypes must match");
+  TORCH_CHECK_VALUE(key_cache.sizes() == value_cache.sizes(), "cache shapes must match");
+  TORCH_CHECK_VALUE(block_mapping.size(1) == 2, "block_mapping must have shape [pairs, 2]");
+  c10::DeviceGuard guard(device);
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(device.index()).stream();
+  const int status = rk_kv_cache_copy(
+      key_cache.data_ptr(), value_cache.data_ptr(), block_mapping.data_ptr(), block_mapping.size(0),
+      key_cache.size(0), key_cache.size(1), key_cache.size(2), key_cache.size(3),
+      key_cache.scalar_type() == at::kBFloat16 ? RK_KV_DTYPE_BF16 : RK_KV_DTYPE_FP16,
+      block_mapping.scalar_type() == at::kLong ? RK_KV_INDEX_INT64 : RK_KV_INDEX_INT32, stream);
+  if (status == RK_KV_ERR_INVALID_ARGUMENT || status == RK_KV_ERR_UNSUPPORTED) {
+    TORCH_CHECK_VALUE(false, "rk_kv: ", rk_kv_last_error());
+  }
+  TORCH_CHECK(status == RK_KV_OK, "rk_kv: ", rk_kv_last_error());
   return {key_cache, value_cache};
 }
 
 }  // namespace
 
-PYBIND11_MODULE(rk_kv_gfx950, module) {
-  module.doc() = "gfx950 paged KV-cache append (16-byte row-chunk gather/scatter)";
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
+  module.doc() = "gfx950 paged KV-cache append (row gather/scatter) and block copy";
   std::string library_path;
   const std::string digest = loaded_kernel_library_digest(&library_path);
   if (digest != kRkKvLibrarySha256) {
-    throw py::import_error("rk_kv_gfx950: kernel library " + library_path + " has SHA-256 " + digest +
+    throw py::import_error("rk_kv: kernel library " + library_path + " has SHA-256 " + digest +
                            ", this module was built against " + kRkKvLibrarySha256);
   }
   module.attr("kernel_library") = library_path;
   module.attr("kernel_library_sha256") = digest;
   module.def("append", &append, "append token K/V rows to their paged-cache slots", py::arg("key"),
              py::arg("value"), py::arg("key_cache"), py::arg("value_cache"), py::arg("slot_mapping"));
+  module.def("copy", &copy, "copy whole cache blocks (source, destination pairs)", py::arg("key_cache"),
+             py::arg("value_cache"), py::arg("block_mapping"));
   module.def("version", []() { return std::string(rk_kv_version()); });
 }

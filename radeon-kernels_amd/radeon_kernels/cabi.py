@@ -143,7 +143,7 @@ def library() -> PagedAttentionLibrary:
 # ---------------------------------------------------------------------------------------------
 # Paged KV-cache library (include/rk_kv_cache.h).
 KV_LIBRARY_PATH = LIBRARY_PATH.parent / "librk_kv_gfx950.so"
-KV_EXPORTED_SYMBOLS = ("rk_kv_cache_append", "rk_kv_last_error", "rk_kv_version")
+KV_EXPORTED_SYMBOLS = ("rk_kv_cache_append", "rk_kv_cache_copy", "rk_kv_last_error", "rk_kv_version")
 RK_KV_OK = 0
 RK_KV_ERR_INVALID_ARGUMENT = 1
 RK_KV_ERR_UNSUPPORTED = 2
@@ -163,6 +163,8 @@ class KvCacheLibrary:
         i64, vp = ctypes.c_int64, ctypes.c_void_p
         lib.rk_kv_cache_append.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int, ctypes.c_int, vp]
         lib.rk_kv_cache_append.restype = ctypes.c_int
+        lib.rk_kv_cache_copy.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int, ctypes.c_int, vp]
+        lib.rk_kv_cache_copy.restype = ctypes.c_int
         lib.rk_kv_last_error.argtypes = []
         lib.rk_kv_last_error.restype = ctypes.c_char_p
         lib.rk_kv_version.argtypes = []
@@ -197,6 +199,33 @@ class KvCacheLibrary:
             kv_heads=kv_heads, head_dim=head_dim, num_blocks=num_blocks, block_size=block_size,
             dtype=RK_DTYPE_BF16 if key.dtype == torch.bfloat16 else RK_DTYPE_FP16,
             index_dtype=RK_INDEX_INT64 if slot_mapping.dtype == torch.int64 else RK_INDEX_INT32,
+            stream=stream.cuda_stream,
+        )
+        if status != RK_KV_OK:
+            raise CabiError(status, self.last_error())
+        return key_cache, value_cache
+
+
+    def copy_raw(self, *, key_cache: int, value_cache: int, block_mapping: int, pairs: int, num_blocks: int,
+                 block_size: int, kv_heads: int, head_dim: int, dtype: int, index_dtype: int, stream: int) -> int:
+        return self.lib.rk_kv_cache_copy(key_cache, value_cache, block_mapping, pairs, num_blocks, block_size,
+                                         kv_heads, head_dim, dtype, index_dtype, stream or None)
+
+    def copy(self, key_cache: Any, value_cache: Any, block_mapping: Any, *, stream: Any | None = None
+             ) -> tuple[Any, Any]:
+        """Launch on torch tensors (all on one GPU); copies blocks in place and returns the caches."""
+
+        import torch
+
+        num_blocks, block_size, kv_heads, head_dim = (int(s) for s in key_cache.shape)
+        if stream is None:
+            stream = torch.cuda.current_stream(key_cache.device)
+        status = self.copy_raw(
+            key_cache=key_cache.data_ptr(), value_cache=value_cache.data_ptr(),
+            block_mapping=block_mapping.data_ptr(), pairs=int(block_mapping.shape[0]), num_blocks=num_blocks,
+            block_size=block_size, kv_heads=kv_heads, head_dim=head_dim,
+            dtype=RK_DTYPE_BF16 if key_cache.dtype == torch.bfloat16 else RK_DTYPE_FP16,
+            index_dtype=RK_INDEX_INT64 if block_mapping.dtype == torch.int64 else RK_INDEX_INT32,
             stream=stream.cuda_stream,
         )
         if status != RK_KV_OK:

@@ -10,8 +10,9 @@ Operators and regions:
 * ``paged_attention_decode``: one exact entry (priority 100) per measured workload shape, with the
   partition size chosen for that shape (``launch.partition_tokens``), and one broad gfx950 region
   (priority 10) covering every shape the library accepts;
-* ``kv_cache_append``: one exact entry per case of the reference's kv_cache_append workload file
-  (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18) and one broad gfx950 region.
+* ``kv_cache_append`` and ``kv_cache_copy``: one exact entry per case of the reference's workload files
+  (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18, kv_cache_copy-1.0.yaml:12-17) and one broad
+  gfx950 region each; their bindings (entrypoints ``append`` and ``copy``) share one kernel library.
 
 Shapes a kernel rejects at launch time (a ValueError) are demoted to the torch fallback by the
 runtime with the reason recorded.  Each operator has its own binding artifact and evidence id; both
@@ -33,7 +34,11 @@ ARTIFACT = "lib/rk_pa_gfx950.so"
 KV_APPEND = "kv_cache_append"
 KV_EVIDENCE_ID = "mi355x-gfx950-kv_cache_append-rowcopy-1"
 KV_ENTRYPOINT = "append"
-KV_ARTIFACT = "lib/rk_kv_gfx950.so"
+KV_ARTIFACT = "lib/rk_kv_append_gfx950.so"
+KV_COPY = "kv_cache_copy"
+KV_COPY_EVIDENCE_ID = "mi355x-gfx950-kv_cache_copy-blockcopy-1"
+KV_COPY_ENTRYPOINT = "copy"
+KV_COPY_ARTIFACT = "lib/rk_kv_copy_gfx950.so"
 
 _INT_MAX = 2**31 - 1
 _POW2_BLOCKS = [1, 2, 4, 8, 16, 32, 64, 128, 256]
@@ -118,6 +123,23 @@ _KV_COMMON = {
 }
 
 
+# kv_cache_copy: (id suffix, workload constraints).  The reference's cases, each for both dtypes.
+KV_COPY_EXACT_REGIONS: list[tuple[str, dict[str, Any]]] = [
+    ("beam-pairs1-gqa8-d128-p16", {"pairs": 1, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 128}),
+    ("beam-pairs8-gqa8-d128-p16", {"pairs": 8, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 128}),
+    ("beam-pairs32-gqa8-d128-p16", {"pairs": 32, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 128}),
+    ("beam-pairs64-gqa8-d256-p16", {"pairs": 64, "num_blocks": 256, "block_size": 16, "kv_heads": 8, "head_dim": 256}),
+    ("beam-pairs32-mha32-d128-p32", {"pairs": 32, "num_blocks": 128, "block_size": 32, "kv_heads": 32, "head_dim": 128}),
+]
+KV_COPY_BROAD_REGION: dict[str, Any] = {
+    "pairs": [1, 1 << 30],
+    "num_blocks": [1, _INT_MAX],
+    "block_size": [1, 1 << 20],
+    "kv_heads": [1, 1 << 20],
+    "head_dim": {"one_of": [64, 128, 256]},
+}
+
+
 def _winner(artifact: str, entrypoint: str, sha256: str) -> dict[str, Any]:
     return {"provider": "native", "artifact": artifact, "entrypoint": entrypoint, "sha256": sha256,
             "format": "python_extension"}
@@ -152,6 +174,12 @@ def render_dispatch_manifest(operator: str, *, environment: dict[str, Any], sha2
                    for suffix, region in KV_EXACT_REGIONS]
         entries.append(_entry(KV_APPEND, "region", 10, environment, {**KV_BROAD_REGION, **_KV_COMMON}, winner, {},
                               KV_EVIDENCE_ID))
+    elif operator == KV_COPY:
+        winner = _winner(KV_COPY_ARTIFACT, KV_COPY_ENTRYPOINT, sha256)
+        entries = [_entry(KV_COPY, suffix, 100, environment, {**region, **_KV_COMMON}, winner, {},
+                          KV_COPY_EVIDENCE_ID) for suffix, region in KV_COPY_EXACT_REGIONS]
+        entries.append(_entry(KV_COPY, "region", 10, environment, {**KV_COPY_BROAD_REGION, **_KV_COMMON}, winner,
+                              {}, KV_COPY_EVIDENCE_ID))
     else:
         raise KeyError(operator)
     return {
@@ -171,6 +199,8 @@ def render_pack_manifest(*, environment: dict[str, Any], digests: dict[str, str]
          **_winner(ARTIFACT, ENTRYPOINT, digests[OPERATOR]), "evidence_id": EVIDENCE_ID},
         {"operator": KV_APPEND, "semantic_version": SEMANTIC_VERSION,
          **_winner(KV_ARTIFACT, KV_ENTRYPOINT, digests[KV_APPEND]), "evidence_id": KV_EVIDENCE_ID},
+        {"operator": KV_COPY, "semantic_version": SEMANTIC_VERSION,
+         **_winner(KV_COPY_ARTIFACT, KV_COPY_ENTRYPOINT, digests[KV_COPY]), "evidence_id": KV_COPY_EVIDENCE_ID},
     ]
     return {
         "schema_version": "1.0",

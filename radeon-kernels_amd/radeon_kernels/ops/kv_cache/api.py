@@ -1,10 +1,11 @@
-"""Public ``kv_cache_append``: write each new token's K/V rows into its paged-cache slot.
+"""Public paged KV-cache operators.
 
-Mirrors src/radeon_kernels/ops/kv_cache/api.py:25-128 in the reference: the same checks in the same
-order with the same messages, the same 10-key dispatch signature, ``native_arguments = (key,
-value, key_cache, value_cache, slot_mapping)``, the fallback label ``torch/index_copy``, and the
-rule that an implementation must hand back the very cache tensors it was given (it writes them in
-place).
+``kv_cache_append`` writes each new token's K/V rows into its cache slot; ``kv_cache_copy`` copies
+whole cache blocks (a beam fork).  Mirrors src/radeon_kernels/ops/kv_cache/api.py:25-215 in the
+reference: the same checks in the same order with the same messages, the same 10-key dispatch
+signatures, ``native_arguments`` = (key, value, key_cache, value_cache, slot_mapping) and
+(key_cache, value_cache, block_mapping), the fallback label ``torch/index_copy``, and the rule that
+an implementation must hand back the very cache tensors it was given (it writes them in place).
 """
 
 from __future__ import annotations
@@ -20,9 +21,10 @@ from radeon_kernels.ops._common import (
     validate_tensor,
 )
 from radeon_kernels.ops._runtime import OperatorRuntime, default_operator_runtime
-from radeon_kernels.ops.kv_cache.reference import kv_cache_append_reference
+from radeon_kernels.ops.kv_cache.reference import kv_cache_append_reference, kv_cache_copy_reference
 
 APPEND = "kv_cache_append"
+COPY = "kv_cache_copy"
 SEMANTIC_VERSION = "1.0"
 LAYOUT = "block_slot_head_dim"
 FALLBACK_SELECTED = "torch/index_copy"
@@ -123,3 +125,60 @@ def kv_cache_append(key: Any, value: Any, key_cache: Any, value_cache: Any, slot
 
     return _execute_append(key, value, key_cache, value_cache, slot_mapping, torch_module=_torch(),
                            runtime=default_operator_runtime())
+
+
+def _execute_copy(
+    key_cache: Any,
+    value_cache: Any,
+    block_mapping: Any,
+    *,
+    torch_module: Any,
+    runtime: OperatorRuntime,
+) -> tuple[Any, Any]:
+    op = COPY
+    num_blocks, block_size, kv_heads, head_dim = _cache_shape(torch_module, key_cache, value_cache, op)
+    validate_index_tensor(torch_module, block_mapping, name="block_mapping", rank=2, operator=op)
+    if block_mapping.device != key_cache.device:
+        raise ValueError(f"{op} block_mapping must use the same device as key_cache")
+    if int(block_mapping.shape[1]) != 2 or int(block_mapping.shape[0]) <= 0:
+        raise ValueError(f"{op} block_mapping must have shape [pairs, 2]")
+    context = tensor_context(torch_module, op, key_cache, value_cache, block_mapping)
+    if not context.contiguous:
+        raise ValueError(f"{op} paged-layout tensors must be contiguous")
+    if context.requires_grad:
+        raise ValueError(f"{op} is inference-only and does not support autograd")
+    signature = {
+        "dtype": context.dtype,
+        "pairs": int(block_mapping.shape[0]),
+        "num_blocks": num_blocks,
+        "block_size": block_size,
+        "kv_heads": kv_heads,
+        "head_dim": head_dim,
+        "index_dtype": index_dtype_name(torch_module, block_mapping.dtype, op),
+        "layout": LAYOUT,
+        "contiguous": context.contiguous,
+        "requires_grad": False,
+    }
+    result = runtime.execute(
+        operator=op,
+        semantic_version=SEMANTIC_VERSION,
+        signature=signature,
+        device_index=context.device_index,
+        torch_module=torch_module,
+        native_arguments=(key_cache, value_cache, block_mapping),
+        fallback=lambda: kv_cache_copy_reference(torch_module, key_cache, value_cache, block_mapping),
+        fallback_selected=FALLBACK_SELECTED,
+    )
+    return _returned_caches(op, result, key_cache, value_cache)
+
+
+def kv_cache_copy(key_cache: Any, value_cache: Any, block_mapping: Any) -> tuple[Any, Any]:
+    """Copy whole cache blocks: block ``block_mapping[i, 0]`` to block ``block_mapping[i, 1]``.
+
+    ``block_mapping`` is ``[pairs, 2]`` (source, destination); destinations must be in range, unique
+    and disjoint from the sources, so every copy reads the pre-call contents.  Updates the caches in
+    place and returns them.
+    """
+
+    return _execute_copy(key_cache, value_cache, block_mapping, torch_module=_torch(),
+                         runtime=default_operator_runtime())

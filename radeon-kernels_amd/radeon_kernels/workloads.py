@@ -223,3 +223,64 @@ def make_append_inputs(case: AppendCase | str, *, dtype: str = "bf16", index_dty
     slots = slots.to(torch.int64 if index_dtype == "int64" else torch.int32).contiguous()
     out = {"key": key, "value": value, "key_cache": key_cache, "value_cache": value_cache, "slot_mapping": slots}
     return {name: tensor.to(device) for name, tensor in out.items()} | {"case": case, "seed": seed}
+
+
+# ---------------------------------------------------------------------------------------------
+# Paged KV-cache block copy: the cases of the reference's workload file
+# (benchmarks/workloads/kv_cache_copy-1.0.yaml:12-17), each in fp16 and bf16.
+@dataclass(frozen=True)
+class CopyCase:
+    key: str
+    pairs: int
+    num_blocks: int
+    block_size: int
+    kv_heads: int
+    head_dim: int
+
+    def block_elements(self) -> int:
+        return self.block_size * self.kv_heads * self.head_dim
+
+    def bytes_moved(self, elem_size: int = 2) -> int:
+        """Algorithmic bytes of one copy: read source K and V blocks, write destination K and V blocks."""
+
+        return 4 * self.pairs * self.block_elements() * elem_size
+
+
+COPY_CASES: dict[str, CopyCase] = {
+    case.key: case
+    for case in (
+        CopyCase("beam-pairs1-gqa8-d128-p16", 1, 256, 16, 8, 128),
+        CopyCase("beam-pairs8-gqa8-d128-p16", 8, 256, 16, 8, 128),
+        CopyCase("beam-pairs32-gqa8-d128-p16", 32, 256, 16, 8, 128),
+        CopyCase("beam-pairs64-gqa8-d256-p16", 64, 256, 16, 8, 256),
+        CopyCase("beam-pairs32-mha32-d128-p32", 32, 128, 32, 32, 128),
+    )
+}
+COPY_SEED = 20261401
+
+
+def make_copy_inputs(case: CopyCase | str, *, dtype: str = "bf16", index_dtype: str = "int64",
+                     seed: int = COPY_SEED, device: Any = "cpu") -> dict[str, Any]:
+    """Seeded inputs of one copy case, generated on the CPU and moved to ``device``.
+
+    Draw order: key cache, value cache (uniform in [-0.5, 0.5)), then one permutation of the block
+    ids whose first ``pairs`` entries are the sources and next ``pairs`` the destinations: unique,
+    in range and disjoint from the sources, as the contract requires
+    (contracts/kv_cache_copy-1.0.json:17; the reference's benchmark uses sources 0..pairs-1 and
+    destinations pairs..2*pairs-1, benchmarks/kv_cache/benchmark.py:115-122).
+    """
+
+    import torch
+
+    if isinstance(case, str):
+        case = COPY_CASES[case]
+    gen = torch.Generator().manual_seed(seed)
+    t_dtype = torch_dtype(torch, dtype)
+    shape = (case.num_blocks, case.block_size, case.kv_heads, case.head_dim)
+    key_cache = (torch.rand(shape, generator=gen, dtype=torch.float32) - 0.5).to(t_dtype)
+    value_cache = (torch.rand(shape, generator=gen, dtype=torch.float32) - 0.5).to(t_dtype)
+    ids = torch.randperm(case.num_blocks, generator=gen)[: 2 * case.pairs]
+    mapping = torch.stack((ids[: case.pairs], ids[case.pairs:]), dim=1)
+    mapping = mapping.to(torch.int64 if index_dtype == "int64" else torch.int32).contiguous()
+    out = {"key_cache": key_cache, "value_cache": value_cache, "block_mapping": mapping}
+    return {name: tensor.to(device) for name, tensor in out.items()} | {"case": case, "seed": seed}

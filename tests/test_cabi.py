@@ -216,3 +216,30 @@ def test_kv_invalid_arguments_are_rejected_before_launch(kvlib, overrides, statu
 def test_kv_missing_library_fails_loudly(tmp_path):
     with pytest.raises(FileNotFoundError, match="build"):
         cabi.KvCacheLibrary(tmp_path / "absent.so")
+
+
+def kv_copy_call(lib, **overrides):
+    args = dict(key_cache=48, value_cache=64, block_mapping=80, pairs=4, num_blocks=16, block_size=16, kv_heads=8,
+                head_dim=128, dtype=cabi.RK_DTYPE_BF16, index_dtype=cabi.RK_INDEX_INT64, stream=0)
+    args.update(overrides)
+    return lib.copy_raw(**args), lib.last_error()
+
+
+@pytest.mark.parametrize(
+    "overrides, status, message",
+    [
+        (dict(key_cache=0), cabi.RK_KV_ERR_INVALID_ARGUMENT, "must not be NULL"),
+        (dict(block_mapping=0), cabi.RK_KV_ERR_INVALID_ARGUMENT, "must not be NULL"),
+        (dict(dtype=9), cabi.RK_KV_ERR_INVALID_ARGUMENT, "dtype"),
+        (dict(index_dtype=-1), cabi.RK_KV_ERR_INVALID_ARGUMENT, "index_dtype"),
+        (dict(pairs=0), cabi.RK_KV_ERR_INVALID_ARGUMENT, "positive"),
+        (dict(value_cache=72), cabi.RK_KV_ERR_UNSUPPORTED, "16-byte aligned"),
+        (dict(block_size=1, kv_heads=1, head_dim=7), cabi.RK_KV_ERR_UNSUPPORTED, "multiple of 16 bytes"),
+        (dict(pairs=(1 << 30) + 1), cabi.RK_KV_ERR_UNSUPPORTED, "2^31"),
+    ],
+)
+@cpu_only
+def test_kv_copy_invalid_arguments_are_rejected_before_launch(kvlib, overrides, status, message):
+    got, text = kv_copy_call(kvlib, **overrides)
+    assert got == status, text
+    assert message in text

@@ -214,7 +214,7 @@ def test_kv_append_cases_select_their_exact_entry(key, dtype, index):
 
     decision = kv_select(kv_signature(APPEND_CASES[key], dtype, index))
     assert decision.entry_id == f"kv_cache_append-gfx950-{key}"
-    assert decision.winner.entrypoint == "append" and decision.winner.artifact == "lib/rk_kv_gfx950.so"
+    assert decision.winner.entrypoint == "append" and decision.winner.artifact == "lib/rk_kv_append_gfx950.so"
     assert decision.evidence_id == dispatch_plan.KV_EVIDENCE_ID
 
 
@@ -247,25 +247,58 @@ def test_kv_entries_merge_into_the_reference_manifest():
         assert decision.entry_id == entry.id
 
 
-def test_pack_lists_both_bindings_and_kv_binding_pins_its_library():
+def test_pack_lists_every_binding_and_kv_bindings_pin_their_library():
     import subprocess
     import sys
 
     pack = KernelPack.from_directory(PACK, verify_artifacts=False)
-    kv_item = pack.get("kv_cache_append", "1.0")
-    manifest = builtin_dispatch_registry().get("kv_cache_append", "1.0")
-    assert all(entry.winner == kv_item.artifact for entry in manifest.entries)
-    binary = PACK / kv_item.artifact.artifact
-    if not binary.is_file():
-        pytest.fail("the kernel pack is not built; run __graft_entry__.build()")
-    assert hashlib.sha256(binary.read_bytes()).hexdigest() == kv_item.artifact.sha256
-    script = (
-        "import importlib.util, torch\n"
-        f"spec = importlib.util.spec_from_file_location('rk_kv_gfx950', r'{binary}')\n"
-        "m = importlib.util.module_from_spec(spec); spec.loader.exec_module(m)\n"
-        "print(m.kernel_library_sha256)\n"
-    )
-    run = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
-    assert run.returncode == 0, run.stderr
     expected = hashlib.sha256((PACK / "lib" / "librk_kv_gfx950.so").read_bytes()).hexdigest()
-    assert run.stdout.strip().splitlines()[-1] == expected
+    for operator in ("kv_cache_append", "kv_cache_copy"):
+        item = pack.get(operator, "1.0")
+        manifest = builtin_dispatch_registry().get(operator, "1.0")
+        assert all(entry.winner == item.artifact for entry in manifest.entries)
+        binary = PACK / item.artifact.artifact
+        if not binary.is_file():
+            pytest.fail("the kernel pack is not built; run __graft_entry__.build()")
+        assert hashlib.sha256(binary.read_bytes()).hexdigest() == item.artifact.sha256
+        script = (
+            "import importlib.util, torch\n"
+            f"spec = importlib.util.spec_from_file_location('{binary.name.split('.')[0]}', r'{binary}')\n"
+            "m = importlib.util.module_from_spec(spec); spec.loader.exec_module(m)\n"
+            f"assert callable(m.{item.artifact.entrypoint})\n"
+            "print(m.kernel_library_sha256)\n"
+        )
+        run = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+        assert run.returncode == 0, run.stderr
+        assert run.stdout.strip().splitlines()[-1] == expected
+
+
+def copy_signature(case, dtype="bf16", index="int64"):
+    from radeon_kernels.ops.kv_cache.api import _execute_copy
+    from test_kv_api import Runtime
+
+    torch_dtype = {"fp16": "float16", "bf16": "bfloat16"}[dtype]
+    cache = FakeTensor((case.num_blocks, case.block_size, case.kv_heads, case.head_dim), dtype=torch_dtype)
+    runtime = Runtime((cache, cache))
+    _execute_copy(cache, cache, FakeTensor((case.pairs, 2), dtype=index), torch_module=FakeTorch(), runtime=runtime)
+    return runtime.call["signature"]
+
+
+@pytest.mark.parametrize("key", sorted(k for k, _ in dispatch_plan.KV_COPY_EXACT_REGIONS))
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_kv_copy_cases_select_their_exact_entry(key, dtype):
+    from radeon_kernels.workloads import COPY_CASES
+
+    decision = Dispatcher(builtin_dispatch_registry()).select(
+        DispatchRequest("kv_cache_copy", "1.0", copy_signature(COPY_CASES[key], dtype)), gfx950_fingerprint())
+    assert decision.entry_id == f"kv_cache_copy-gfx950-{key}"
+    assert decision.winner.entrypoint == "copy" and decision.winner.artifact == "lib/rk_kv_copy_gfx950.so"
+
+
+def test_kv_copy_entries_merge_into_the_reference_manifest():
+    reference = json.loads((GOLDEN / "reference_dispatch_kv_cache_copy-1.0.json").read_text())
+    ours = json.loads((ROOT / "radeon-kernels_amd" / "radeon_kernels" / "dispatch" / "kv_cache_copy-1.0.json").read_text())
+    merged = copy.deepcopy(reference)
+    merged["entries"].extend(ours["entries"])
+    parsed = DispatchManifest.from_mapping(merged, "merged")
+    assert len(parsed.entries) == len(reference["entries"]) + len(ours["entries"])

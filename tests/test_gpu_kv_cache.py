@@ -1,4 +1,5 @@
-"""GPU parity of the gfx950 paged KV-cache append (bit-exact, contracts/kv_cache_append-1.0.json:21).
+"""GPU parity of the gfx950 paged KV-cache append and block copy (bit-exact: contracts/kv_cache_append-1.0.json:21,
+contracts/kv_cache_copy-1.0.json:21).
 
 * every case of the reference's workload file (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18),
   both dtypes, both index types, through the C ABI and through ``rk.kv_cache_append`` (which must
@@ -6,7 +7,9 @@
 * out-of-range and negative slots are skipped and nothing else changes;
 * HIP graph capture: every replay (with new token data each time) matches the oracle;
 * append then decode: tokens written by the append are read by the decode exactly where the block
-  tables put them (the two halves of a decode step, on the same cache layout).
+  tables put them (the two halves of a decode step, on the same cache layout);
+* block copy: every case of kv_cache_copy-1.0.yaml, both dtypes and index types, through the C ABI;
+  ``rk.kv_cache_copy`` selects the gfx950 winner; pairs with an out-of-range block are skipped.
 """
 
 from __future__ import annotations
@@ -149,3 +152,54 @@ def test_append_then_decode_reads_the_new_tokens(gpu, kvlib, palib):
                        dev["context_lengths"], partition_tokens=32)
     torch.cuda.synchronize()
     assert_within(out, oracle64(updated), "bf16", "append then decode")
+
+
+# ---------------------------------------------------------------------------------------------
+# Block copy (contracts/kv_cache_copy-1.0.json: bit-exact, snapshot semantics)
+from radeon_kernels.workloads import COPY_CASES, CopyCase, make_copy_inputs  # noqa: E402
+
+
+def expected_copy_bits(data):
+    b = kv_oracle.as_bits
+    return kv_oracle.copy_numpy(b(data["key_cache"]), b(data["value_cache"]), data["block_mapping"].cpu().numpy())
+
+
+@pytest.mark.parametrize("case", sorted(COPY_CASES))
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("index_dtype", ["int32", "int64"])
+def test_copy_cases_bit_exact_through_the_c_abi(gpu, kvlib, case, dtype, index_dtype):
+    import torch
+
+    data = make_copy_inputs(case, dtype=dtype, index_dtype=index_dtype)
+    expected = expected_copy_bits(data)
+    dev = {k: v.to(gpu) for k, v in data.items() if hasattr(v, "to")}
+    announce(f"kv copy {case} {dtype} {index_dtype}")
+    kc, vc = kvlib.copy(dev["key_cache"], dev["value_cache"], dev["block_mapping"])
+    torch.cuda.synchronize()
+    assert_caches(kc, vc, expected, f"copy {case}/{dtype}/{index_dtype}")
+
+
+def test_public_copy_selects_the_gfx950_kernel_and_skips_out_of_range_pairs(gpu, kvlib):
+    import torch
+
+    import radeon_kernels as rk
+
+    data = make_copy_inputs("beam-pairs32-mha32-d128-p32", dtype="bf16", index_dtype="int64")
+    expected = expected_copy_bits(data)
+    dev = {k: v.to(gpu) for k, v in data.items() if hasattr(v, "to")}
+    announce("rk.kv_cache_copy beam-pairs32-mha32")
+    kc, vc = rk.kv_cache_copy(dev["key_cache"], dev["value_cache"], dev["block_mapping"])
+    torch.cuda.synchronize()
+    record = rk.get_last_dispatch()
+    assert record["selected"] == "native/copy", rk.explain_last_dispatch()
+    assert record["entry_id"] == "kv_cache_copy-gfx950-beam-pairs32-mha32-d128-p32"
+    assert_caches(kc, vc, expected, "public copy")
+
+    small = make_copy_inputs(CopyCase("edge", 3, 12, 16, 2, 64), dtype="fp16", index_dtype="int32", seed=8)
+    small["block_mapping"] = torch.tensor([[1, 5], [2, 12], [-1, 6], [3, 0], [11, -4]], dtype=torch.int32)
+    expected = expected_copy_bits(small)
+    dev = {k: v.to(gpu) for k, v in small.items() if hasattr(v, "to")}
+    announce("kv copy out-of-range pairs")
+    kvlib.copy(dev["key_cache"], dev["value_cache"], dev["block_mapping"])
+    torch.cuda.synchronize()
+    assert_caches(dev["key_cache"], dev["value_cache"], expected, "out-of-range pairs")

@@ -82,3 +82,42 @@ def test_implementation_must_return_the_given_caches():
     with pytest.raises(RuntimeError, match="must return the input cache tensors"):
         append(result=(Other((256, 16, 8, 128)), Other((256, 16, 8, 128))),
                key_cache=Same((256, 16, 8, 128)), value_cache=Same((256, 16, 8, 128)))
+
+
+# ---------------------------------------------------------------------------------------------
+from radeon_kernels.ops.kv_cache.api import _execute_copy  # noqa: E402
+
+
+def copy(cache=(128, 32, 32, 128), mapping=(8, 2), *, dtype="bfloat16", index="int32", **overrides):
+    key_cache = overrides.pop("key_cache", FakeTensor(cache, dtype=dtype))
+    value_cache = overrides.pop("value_cache", FakeTensor(cache, dtype=dtype))
+    block_mapping = overrides.pop("block_mapping", FakeTensor(mapping, dtype=index))
+    runtime = Runtime((key_cache, value_cache))
+    out = _execute_copy(key_cache, value_cache, block_mapping, torch_module=FakeTorch(), runtime=runtime)
+    return out, runtime.call
+
+
+def test_copy_signature_matches_the_reference_unit_test():
+    _, call = copy()
+    assert call["operator"] == "kv_cache_copy"
+    assert call["signature"] == {
+        "dtype": "bf16", "pairs": 8, "num_blocks": 128, "block_size": 32, "kv_heads": 32, "head_dim": 128,
+        "index_dtype": "int32", "layout": "block_slot_head_dim", "contiguous": True, "requires_grad": False,
+    }
+    assert len(call["native_arguments"]) == 3 and call["fallback_selected"] == "torch/index_copy"
+
+
+@pytest.mark.parametrize(
+    "kwargs, error, message",
+    [
+        (dict(block_mapping=FakeTensor((1, 2))), TypeError, "index tensors"),
+        (dict(mapping=(4, 3)), ValueError, r"shape \[pairs, 2\]"),
+        (dict(block_mapping=FakeTensor((4,), dtype="int64")), ValueError, "rank 2"),
+        (dict(value_cache=FakeTensor((128, 32, 32, 64), dtype="bfloat16")), ValueError, "same shape"),
+        (dict(key_cache=FakeTensor((128, 32, 32, 128), dtype="bfloat16", contiguous=False)), ValueError,
+         "must be contiguous"),
+    ],
+)
+def test_copy_validation_messages(kwargs, error, message):
+    with pytest.raises(error, match=message):
+        copy(**kwargs)

@@ -1,4 +1,4 @@
-"""Pinning the KV-cache append oracle (oracle/kv_oracle.py) before trusting it as the checker.
+"""Pinning the KV-cache oracles (oracle/kv_oracle.py) before trusting them as the checkers.
 
 What pins the reference algorithm (src/radeon_kernels/ops/kv_cache/reference.py:6-20):
 
@@ -10,8 +10,12 @@ What pins the reference algorithm (src/radeon_kernels/ops/kv_cache/reference.py:
 * invariants: slots not named by ``slot_mapping`` keep their bytes; gathering the named slots
   returns the input rows; the token order of (key, value, slot) triples does not matter.
 
-The product's own torch fallback (``radeon_kernels.ops.kv_cache.reference``) is checked against the
-oracle too, and planted mistakes in copies of the oracle each fail one of the checks above.
+The block copy (reference.py:23-38) is pinned the same way: torch's ``index_select`` +
+``index_copy_`` snapshot on every case of kv_cache_copy-1.0.yaml, untouched blocks, skipped
+out-of-range pairs and a chained mapping that only a snapshot gets right.
+
+The product's own torch fallbacks (``radeon_kernels.ops.kv_cache.reference``) are checked against
+the oracle too, and planted mistakes in copies of the oracle each fail one of the checks above.
 """
 
 from __future__ import annotations
@@ -150,3 +154,82 @@ def test_planted_mistakes_are_caught(kind):
 
 def test_unmutated_restatement_passes_the_same_checks():
     assert _pinning_checks(_mutant("none")) == []
+
+
+# ---------------------------------------------------------------------------------------------
+# Block copy (reference.py:23-38)
+from radeon_kernels.ops.kv_cache.reference import kv_cache_copy_reference  # noqa: E402
+from radeon_kernels.workloads import COPY_CASES, CopyCase, make_copy_inputs  # noqa: E402
+
+
+def copy_args(data):
+    return bits(data["key_cache"]), bits(data["value_cache"]), data["block_mapping"].numpy()
+
+
+def torch_snapshot_copy(data):
+    """Library routines: index_select the sources, then index_copy_ into the destinations."""
+
+    kc, vc = data["key_cache"].clone(), data["value_cache"].clone()
+    mapping = data["block_mapping"].to(torch.int64)
+    k_src, v_src = kc.index_select(0, mapping[:, 0]), vc.index_select(0, mapping[:, 0])
+    kc.index_copy_(0, mapping[:, 1], k_src)
+    vc.index_copy_(0, mapping[:, 1], v_src)
+    return bits(kc), bits(vc)
+
+
+@pytest.mark.parametrize("case", sorted(COPY_CASES))
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("index_dtype", ["int32", "int64"])
+def test_copy_oracle_matches_torch_snapshot_copy(case, dtype, index_dtype):
+    data = make_copy_inputs(case, dtype=dtype, index_dtype=index_dtype)
+    got = kv_oracle.copy_numpy(*copy_args(data))
+    ref = torch_snapshot_copy(data)
+    assert all(np.array_equal(x, y) for x, y in zip(got, ref))
+
+
+def test_copy_invariants_and_out_of_range_pairs():
+    data = make_copy_inputs(CopyCase("small", 3, 10, 4, 2, 8), dtype="fp16", seed=4)
+    data["block_mapping"] = torch.tensor([[1, 7], [2, 10], [-1, 3], [4, 0]], dtype=torch.int64)
+    k, v = kv_oracle.copy_numpy(*copy_args(data))
+    before_k = bits(data["key_cache"])
+    assert np.array_equal(k[7], before_k[1]) and np.array_equal(k[0], before_k[4])
+    untouched = [b for b in range(10) if b not in (7, 0)]
+    assert np.array_equal(k[untouched], before_k[untouched])
+    # Chained mapping (outside the contract): snapshot semantics read pre-call sources.
+    chain = dict(data, block_mapping=torch.tensor([[1, 2], [2, 3]], dtype=torch.int64))
+    k2, _ = kv_oracle.copy_numpy(*copy_args(chain))
+    assert np.array_equal(k2[3], before_k[2]) and np.array_equal(k2[2], before_k[1])
+    assert all(np.array_equal(x, y) for x, y in zip(kv_oracle.copy_numpy(*copy_args(chain)), torch_snapshot_copy(chain)))
+
+
+def test_product_copy_fallback_matches_oracle():
+    data = make_copy_inputs("beam-pairs32-mha32-d128-p32", dtype="bf16", index_dtype="int32")
+    expected = kv_oracle.copy_numpy(*copy_args(data))
+    kc, vc = data["key_cache"].clone(), data["value_cache"].clone()
+    out = kv_cache_copy_reference(torch, kc, vc, data["block_mapping"])
+    assert out[0] is kc and out[1] is vc
+    assert np.array_equal(bits(kc), expected[0]) and np.array_equal(bits(vc), expected[1])
+
+
+def _copy_mutant(kind):
+    def copy(key_cache, value_cache, block_mapping):
+        k_out, v_out = key_cache.copy(), value_cache.copy()
+        for s, d in np.asarray(block_mapping).tolist():
+            if kind == "direction_swapped":
+                s, d = d, s
+            k_out[d] = key_cache[s]
+            v_out[d] = key_cache[s] if kind == "value_from_key" else value_cache[s]
+            if kind == "first_slot_only":
+                k_out[d, 1:] = key_cache[d, 1:]
+        return k_out, v_out
+
+    return copy
+
+
+@pytest.mark.parametrize("kind", ["direction_swapped", "value_from_key", "first_slot_only"])
+def test_copy_planted_mistakes_are_caught(kind):
+    data = make_copy_inputs("beam-pairs8-gqa8-d128-p16", dtype="bf16")
+    got = _copy_mutant(kind)(*copy_args(data))
+    assert not all(np.array_equal(x, y) for x, y in zip(got, torch_snapshot_copy(data)))
+    clean = _copy_mutant("none")(*copy_args(data))
+    assert all(np.array_equal(x, y) for x, y in zip(clean, torch_snapshot_copy(data)))

@@ -1,8 +1,10 @@
 #!/usr/bin/env python3
 """Paged-attention decode benchmark on one MI355X (gfx950).
 
-One step = one decode call (partition kernel + partition-reduce kernel) over the whole batch of the
-workload, inputs resident in HBM.  Default workload: 128 sequences, 32 query / 8 KV heads, head_dim
+One step = one decode call over the whole batch of the workload, inputs resident in HBM, in the form
+the workload's dispatch entry selects (launch.merge): "reduce" -- the partition kernel followed by the
+partition-reduce kernel -- or "fused" -- the partition kernel alone, its last workgroup per sequence
+and head slot merging the partition records.  --merge overrides the entry.  Default workload: 128 sequences, 32 query / 8 KV heads, head_dim
 128, block 16, bf16, context lengths ~ U[1024, 16384] (seeded), about 4.8 GB of K/V per call -- 18x
 the 256 MB last-level cache, so every call streams from HBM.
 
@@ -12,14 +14,18 @@ Prints one JSON line:
                    else on the stream (us_per_call_events: the same region by HIP events)
   roofline         the partition kernel against the 8 TB/s HBM peak: achieved = KV bytes / its
                    average duration, from HIP events recorded on the launch stream around K
-                   back-to-back launches of that kernel alone; traffic = measured HBM bytes per
-                   launch from the committed rocprofv3 counter summary for this exact
-                   configuration (null when there is none)
+                   back-to-back launches of that kernel alone (in the fused form the call is that
+                   one kernel); traffic = measured HBM bytes per launch from the committed
+                   rocprofv3 counter summary for this exact configuration (null when there is none)
+  kernels_us       per-launch averages of the reduce form's two kernels; us_per_call_reduce and
+                   us_per_call_fused time both whole-call forms (omitted with --no-breakdown, which
+                   times the headline form only)
   cpu_baseline     the reference algorithm (its torch fallback, restated in oracle/) on the host
                    cores over a bounded sample of the same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5] [--variant mfma]
-                       [--partition P] [--no-cpu-baseline] [--cpu-seconds S] [--calibration-copy]
+                       [--partition P] [--merge fused|reduce] [--no-breakdown] [--no-cpu-baseline]
+                       [--cpu-seconds S] [--calibration-copy]
        python bench.py --operator kv_cache_append|kv_cache_copy [--case ...] [--dtype bf16]
                        (the paged-cache operators around the decode; same JSON line shape)
 """
@@ -52,6 +58,10 @@ def parse_args(argv=None):
     parser.add_argument("--workload", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
     parser.add_argument("--variant", default=None, choices=["mfma", "valu"])
     parser.add_argument("--partition", type=int, default=None)
+    parser.add_argument("--merge", default=None, choices=["fused", "reduce"],
+                        help="partition-record merge form (default: the workload's dispatch entry)")
+    parser.add_argument("--no-breakdown", action="store_true",
+                        help="time only the headline call (no per-kernel breakdown of the other form)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--calibration-copy", action="store_true",
@@ -83,8 +93,8 @@ def public_call_us(torch, call, steps: int, batches: int = 5) -> float:
     return statistics.median(times)
 
 
-def dispatch_launch(workload_key: str) -> tuple[str, int]:
-    """Entrypoint and partition size the gfx950 dispatch table assigns to this workload."""
+def dispatch_launch(workload_key: str) -> tuple[str, int, str]:
+    """Entrypoint, partition size and merge form the gfx950 dispatch table assigns to this workload."""
 
     from radeon_kernels import dispatch_plan
 
@@ -93,12 +103,13 @@ def dispatch_launch(workload_key: str) -> tuple[str, int]:
              "c5": "b128-gqa32x8-ragged-d128-p16-bf16"}
     for suffix, _, launch in dispatch_plan.EXACT_REGIONS:
         if suffix == names[workload_key]:
-            return dispatch_plan.ENTRYPOINT, int(launch["partition_tokens"])
+            return dispatch_plan.ENTRYPOINT, int(launch["partition_tokens"]), str(launch["merge"])
     raise KeyError(workload_key)
 
 
-def read_traffic(workload: str, variant: str, partition: int):
-    """HBM bytes per partition-kernel launch from the committed counter summary, if it matches."""
+def read_traffic(workload: str, variant: str, partition: int, merge: str = "reduce"):
+    """HBM bytes per partition-kernel launch from the committed counter summary, if it matches
+    (``merge``: the form the summary was measured in; a summary without the field is "reduce")."""
 
     if not TRAFFIC_SUMMARY.is_file():
         return None
@@ -108,7 +119,8 @@ def read_traffic(workload: str, variant: str, partition: int):
             key, value = line.split("=", 1)
             fields[key.strip()] = value.strip()
     try:
-        if fields.get("workload") != workload or fields.get("variant") != variant or int(fields["partition_tokens"]) != partition:
+        if (fields.get("workload") != workload or fields.get("variant") != variant
+                or int(fields["partition_tokens"]) != partition or fields.get("merge", "reduce") != merge):
             return None
         return int(fields["hbm_bytes_per_launch"])
     except (KeyError, ValueError):
@@ -316,9 +328,10 @@ def main(argv=None) -> int:
     arch = torch.cuda.get_device_properties(0).gcnArchName.split(":", 1)[0]
     lib = library()  # raises if the HIP library was not built
     w = WORKLOADS[args.workload]
-    entrypoint, planned_partition = dispatch_launch(args.workload)
+    entrypoint, planned_partition, planned_merge = dispatch_launch(args.workload)
     variant = args.variant or entrypoint.split("_", 1)[1]
     partition = args.partition or planned_partition
+    merge = args.merge or planned_merge
 
     if args.calibration_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
@@ -343,16 +356,17 @@ def main(argv=None) -> int:
     need = lib.workspace_bytes(batch, hq, d, bs, mb, partition)
     out = torch.empty_like(q)
     workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    counters = torch.zeros(lib.counter_words(batch, hq, hkv), dtype=torch.int32, device=device)
     stream = torch.cuda.current_stream(device)
+    headline = "fused" if merge == "fused" else "all"
 
     def launch(phase: str, k, v):
         lib.decode(q, k, v, bt, cl, partition_tokens=partition, variant=variant, out=out, workspace=workspace,
-                   stream=stream, phase=phase)
+                   stream=stream, phase=phase, counters=counters)
 
     for i in range(args.warmup):
         k, v = caches[i % copies]
-        launch("partitions", k, v)
-        launch("reduce", k, v)
+        launch(headline, k, v)
     torch.cuda.synchronize()
 
     def region(phase: str) -> tuple[float, float]:
@@ -372,15 +386,23 @@ def main(argv=None) -> int:
         wall = time.perf_counter() - t
         return start.elapsed_time(end) * 1e3 / args.steps, wall * 1e6 / args.steps
 
-    # The contract's timed region: K whole decode calls (partition kernel, then reduce kernel when
-    # the shape needs one), nothing else on the stream.  Then each kernel on its own, K launches
-    # each, for its average duration (the roofline figure).
-    event_us, us_per_call = region("all")
-    part_avg, _ = region("partitions")
-    # One partition covering every sequence needs no reduce launch (the call launches one kernel).
-    red_avg = region("reduce")[0] if need > 0 else None
+    # The contract's timed region: K whole decode calls, nothing else on the stream.  In the fused
+    # form that is K launches of the partition kernel (its average duration is the roofline
+    # figure).  The breakdown times each kernel of the reduce form on its own, K launches each
+    # (the reduce form's roofline figure is its partition kernel), and the other whole-call form.
+    event_us, us_per_call = region(headline)
+    part_avg = red_avg = None
+    forms = {merge: us_per_call}
+    if not args.no_breakdown or merge == "reduce":
+        part_avg, _ = region("partitions")
+        # One partition covering every sequence needs no reduce launch (the call launches one kernel).
+        red_avg = region("reduce")[0] if need > 0 else None
+    if not args.no_breakdown:
+        other = "reduce" if merge == "fused" else "fused"
+        forms[other] = region("fused" if other == "fused" else "all")[1]
+    kernel_avg = part_avg if merge == "reduce" else event_us
     gbps = kv_bytes / (us_per_call * 1e3)
-    achieved = kv_bytes / (part_avg * 1e3)
+    achieved = kv_bytes / (kernel_avg * 1e3)
 
     hot = None
     if copies > 1:  # the same cache every call: last-level-cache resident
@@ -388,7 +410,7 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         t = time.perf_counter()
         for _ in range(args.steps):
-            launch("all", k, v)
+            launch(headline, k, v)
         torch.cuda.synchronize()
         hot = round((time.perf_counter() - t) / args.steps * 1e6, 2)
 
@@ -407,7 +429,7 @@ def main(argv=None) -> int:
     decision = rk.get_last_dispatch()
     rk_us = public_call_us(torch, lambda: rk.paged_attention_decode(q, k, v, bt, cl), max(1, args.steps // 5))
 
-    traffic = read_traffic(w.name, variant, partition)
+    traffic = read_traffic(w.name, variant, partition, merge)
     result = {
         "metric": METRIC,
         "value": round(gbps, 1),
@@ -427,14 +449,18 @@ def main(argv=None) -> int:
             "block_size": int(bs), "num_blocks": int(nb), "max_blocks_per_sequence": int(mb),
             "context": list(w.context) if w.ragged else w.context, "seed": data["seed"],
             "entrypoint": f"decode_{variant}", "partition_tokens": partition, "kv_copies_rotated": copies,
+            "merge": merge,
             "arch": arch,
         },
         "us_per_call": round(us_per_call, 2),
         "us_per_call_events": round(event_us, 2),
         "pct_hbm_peak": round(gbps / HBM_PEAK_GBPS * 100, 2),
         "kv_bytes_per_call": kv_bytes,
-        "kernels_us": {"pa_partition_kernel": round(part_avg, 2),
-                       "pa_reduce_kernel": None if red_avg is None else round(red_avg, 2)},
+        "kernels_us": None if part_avg is None else {
+            "pa_partition_kernel": round(part_avg, 2),
+            "pa_reduce_kernel": None if red_avg is None else round(red_avg, 2)},
+        "us_per_call_reduce": round(forms["reduce"], 2) if "reduce" in forms else None,
+        "us_per_call_fused": round(forms["fused"], 2) if "fused" in forms else None,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

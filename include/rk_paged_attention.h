@@ -15,6 +15,10 @@
  *                           -> no reference counterpart: the reference kernel has no context split.
  *                              The caller sizes the split-K partial buffer with it (the torch
  *                              extension allocates it from the caching allocator).
+ *   rk_pa_decode_fused, rk_pa_decode_counter_words
+ *                           -> no reference counterpart: the single-launch form of rk_pa_decode for
+ *                              callers that keep a small persistent counter buffer per stream
+ *                              (the torch extension does).
  *   rk_pa_last_error, rk_pa_version
  *                           -> error text that TORCH_CHECK carried in the reference
  *                              (native_paged_attention.hip:199-219,239-240).
@@ -115,6 +119,29 @@ int rk_pa_decode_reduce(const void* query, const void* key_cache, const void* va
                         int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_sequence,
                         float scale, int dtype, int index_dtype, int64_t partition_tokens,
                         int variant, void* stream);
+
+/*
+ * Single-launch decode (no reference counterpart): the partition kernel merges the partition
+ * records itself.  The last workgroup to finish a (sequence, KV head, head chunk) counts its arrival
+ * on a device-scope atomic counter, sees that it was last, and merges the records of every
+ * partition of that sequence in partition order; no reduce launch follows.  Results agree with
+ * rk_pa_decode to fp32 rounding of the final merge (both are deterministic).
+ *
+ * counters/counter_words: device array of at least rk_pa_decode_counter_words(...) uint32 words.
+ *   It must be all zero before the first call (e.g. hipMemset once at allocation); every call
+ *   that completes leaves it all zero again, so one buffer serves any number of calls in stream
+ *   order.  Calls that may run concurrently (different streams) need separate counter buffers
+ *   and separate workspaces.  Ignored (may be NULL) when rk_pa_decode_workspace_bytes is zero.
+ * All other arguments are those of rk_pa_decode.
+ */
+int rk_pa_decode_counter_words(int64_t batch, int64_t query_heads, int64_t kv_heads, size_t* words);
+int rk_pa_decode_fused(const void* query, const void* key_cache, const void* value_cache,
+                       const void* block_tables, const void* context_lengths, void* output,
+                       void* workspace, size_t workspace_bytes, uint32_t* counters,
+                       size_t counter_words, int64_t batch, int64_t query_heads, int64_t kv_heads,
+                       int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                       int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
+                       int64_t partition_tokens, int variant, void* stream);
 
 /* Text describing the last non-RK_OK status returned on the calling thread. */
 const char* rk_pa_last_error(void);

@@ -241,6 +241,9 @@ struct Params {
   uint16_t* __restrict__ out;
   float* __restrict__ ws_acc;  // [batch, query_heads, num_partitions, D]
   float* __restrict__ ws_ml;   // [batch, query_heads, num_partitions, 2] = (max, sum)
+  // Fused merge only (else null): [batch, kv_heads * head_chunks] arrival counters, zero on entry,
+  // left zero on exit (the last arriver resets its counter).
+  uint32_t* __restrict__ counters;
   int64_t block_stride;        // elements between physical blocks: BS * Hkv * D
   int64_t row_stride;          // elements between slots of a block: Hkv * D
   int32_t batch;
@@ -262,6 +265,127 @@ __device__ __forceinline__ int64_t clamped_context(const Params& p, int b) {
   const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << p.bs_log2;
   const int64_t ctx = load_index(p.context_lengths, b, p.index_is64 != 0);
   return ctx < max_ctx ? ctx : max_ctx;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Partition merge of one (sequence, query head) row by one wave.  The global maximum comes from a
+// wave-wide max over the partition maxima; each lane then owns one record's weight
+// exp2(m_i - M), the sum is a wave-wide sum of l_i * weight, and the accumulator columns are
+// merged in partition-index order, a group of records at a time with all their loads issued
+// together.  Fixed order and fixed grouping make the result deterministic, and the reduce kernel
+// and the fused epilogue of the partition kernel run this same code, so both give bit-identical
+// outputs.
+//
+// Records cross XCDs (each XCD has its own L2).  They are stored with agent-scope atomic stores
+// (write-through to the device coherence point, no dirty L2 lines) and, inside the fused epilogue,
+// read with agent-scope atomic loads (fetched from the coherence point, never from a stale line of
+// this XCD's L2).  Neither needs the whole-L2 write-back or invalidate that an agent-scope fence
+// performs; ordering between the stores and the arrival counter comes from waiting for the stores'
+// acknowledgements before the counter is incremented.
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) x = fmaxf(x, __shfl_xor(x, offset));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) x += __shfl_xor(x, offset);
+  return x;
+}
+
+__device__ __forceinline__ void store_record(float* ptr, float x) {
+  __hip_atomic_store(ptr, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ float load_record(const float* ptr) {
+  if constexpr (COHERENT) {
+    return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    return *ptr;  // after a kernel boundary: the launch order already makes the records visible
+  }
+}
+
+template <class E, int D, bool COHERENT>
+__device__ __forceinline__ void merge_partitions(const Params& p, int64_t row, int np, int lane) {
+  constexpr int PER_LANE = D / kWave;
+  constexpr int GROUP = 32 / PER_LANE;  // 32 accumulator loads in flight per lane; divides 64
+  const float* ml = p.ws_ml + row * p.num_partitions * 2;
+  const float* acc = p.ws_acc + row * p.num_partitions * D;
+  const float neg_inf = -__builtin_inff();
+  // Accumulator columns of records i0 .. i0 + GROUP - 1 (an index past np re-reads the last record;
+  // its weight is 0 and fmaf(v, 0, A) == A, so the padding leaves the sum unchanged).
+  auto load_group = [&](float (&vals)[GROUP][PER_LANE], int i0) {
+#pragma unroll
+    for (int u = 0; u < GROUP; ++u) {
+      const int64_t i = min(i0 + u, np - 1);
+#pragma unroll
+      for (int c = 0; c < PER_LANE; ++c) vals[u][c] = load_record<COHERENT>(acc + i * D + lane + c * kWave);
+    }
+  };
+
+  // One memory round: lane j's own (max, sum) record j and the first group of accumulators.
+  float m_lane = neg_inf, l_lane = 0.0f;
+  if (lane < np) {
+    m_lane = load_record<COHERENT>(ml + 2 * lane);
+    l_lane = load_record<COHERENT>(ml + 2 * lane + 1);
+  }
+  float vals[GROUP][PER_LANE];
+  load_group(vals, 0);
+  float M = fmaxf(neg_inf, m_lane);
+  for (int i = lane + kWave; i < np; i += kWave) M = fmaxf(M, load_record<COHERENT>(ml + 2 * i));
+  M = wave_max(M);
+
+  // Records in chunks of 64: lane j computes the weight of record c0 + j (0 past np), the sum
+  // accumulates per lane, and the accumulator columns take the weights in record order by
+  // broadcast from the owning lane.
+  float L = 0.0f;
+  float A[PER_LANE];
+#pragma unroll
+  for (int c = 0; c < PER_LANE; ++c) A[c] = 0.0f;
+  for (int c0 = 0; c0 < np; c0 += kWave) {
+    float mi = m_lane, li = l_lane;
+    if (c0 > 0) {
+      mi = neg_inf;
+      li = 0.0f;
+      if (c0 + lane < np) {
+        mi = load_record<COHERENT>(ml + 2 * (c0 + lane));
+        li = load_record<COHERENT>(ml + 2 * (c0 + lane) + 1);
+      }
+    }
+    const float f = (mi == neg_inf) ? 0.0f : fast_exp2(mi - M);
+    L += (mi == neg_inf) ? 0.0f : li * f;
+    const int n = min(kWave, np - c0);
+    for (int u0 = 0; u0 < n; u0 += GROUP) {
+      if (c0 + u0 > 0) load_group(vals, c0 + u0);
+#pragma unroll
+      for (int u = 0; u < GROUP; ++u) {
+        const float fu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), u0 + u));
+#pragma unroll
+        for (int c = 0; c < PER_LANE; ++c) A[c] = fmaf(vals[u][c], fu, A[c]);
+      }
+    }
+  }
+  L = wave_sum(L);
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int c = 0; c < PER_LANE; ++c) p.out[row * D + lane + c * kWave] = E::store(A[c] * inv);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Partition reduce: one wave per (sequence, query head), for rows whose sequence spans several
+// partitions (the partition kernel writes the others itself).
+template <class E, int D>
+__global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= static_cast<int64_t>(p.batch) * p.query_heads) return;
+  const int b = static_cast<int>(row / p.query_heads);
+  const int64_t ctx = clamped_context(p, b);
+  if (ctx <= 0) return;  // written by the partition kernel
+  const int np = static_cast<int>((ctx + p.partition_tokens - 1) / p.partition_tokens);
+  if (np <= 1) return;   // written by the partition kernel
+  merge_partitions<E, D, false>(p, row, np, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -315,6 +439,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   __shared__ int s_table[kMaxSliceBlocks];
   __shared__ float s_m[kWaves][GC];
   __shared__ float s_l[kWaves][GC];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -824,81 +949,33 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
       p.out[row * D + d] = E::store(A / L);
     } else {
       const int64_t rec = row * p.num_partitions + part;
-      p.ws_acc[rec * D + d] = A;
+      store_record(p.ws_acc + rec * D + d, A);
       if (d == 0) {
-        p.ws_ml[rec * 2] = M;
-        p.ws_ml[rec * 2 + 1] = L;
+        store_record(p.ws_ml + rec * 2, M);
+        store_record(p.ws_ml + rec * 2 + 1, L);
       }
     }
   }
-}
+  if (single || p.counters == nullptr) return;
 
-// ---------------------------------------------------------------------------------------------
-// Partition reduce: one wave per (sequence, query head).  The global maximum comes from a
-// wave-wide max over the partition maxima; the records are then merged in partition-index order,
-// eight at a time with all their loads issued together (a record past the last partition is
-// re-read from the last one and weighted by 0, keeping the loads unconditional).  Fixed order and
-// fixed grouping make the result deterministic.
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) x = fmaxf(x, __shfl_xor(x, offset));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) x += __shfl_xor(x, offset);
-  return x;
-}
-
-template <class E, int D>
-__global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
-  constexpr int PER_LANE = D / kWave;
-  constexpr int GROUP = 8;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= static_cast<int64_t>(p.batch) * p.query_heads) return;
-  const int b = static_cast<int>(row / p.query_heads);
-  const int64_t ctx = clamped_context(p, b);
-  if (ctx <= 0) return;  // written by the partition kernel
-  const int np = static_cast<int>((ctx + p.partition_tokens - 1) / p.partition_tokens);
-  if (np <= 1) return;   // written by the partition kernel
-  const float* ml = p.ws_ml + row * p.num_partitions * 2;
-  const float* acc = p.ws_acc + row * p.num_partitions * D;
-  const float neg_inf = -__builtin_inff();
-
-  float M = neg_inf;
-  for (int i = lane; i < np; i += kWave) M = fmaxf(M, ml[2 * i]);
-  M = wave_max(M);
-  float L = 0.0f;
-  for (int i = lane; i < np; i += kWave) {
-    const float mi = ml[2 * i];
-    L += (mi == neg_inf) ? 0.0f : ml[2 * i + 1] * fast_exp2(mi - M);
+  // Fused merge.  Every wave waits until its record stores (agent-scope, written through) are
+  // acknowledged; after the barrier one thread counts the workgroup's arrival on the (sequence,
+  // head slot) counter.  The last of the np arrivals resets the counter for the next call and merges
+  // every partition of its heads in partition order, reading the records with agent-scope loads.
+  // Nobody waits for anybody, so no workgroup depends on another being scheduled.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the record stores above the wait
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* counter = p.counters + static_cast<int64_t>(b) * heads_per_seq + hslot;
+    const uint32_t prior = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prior == static_cast<uint32_t>(np - 1);
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
   }
-  L = wave_sum(L);
-
-  float A[PER_LANE];
-#pragma unroll
-  for (int c = 0; c < PER_LANE; ++c) A[c] = 0.0f;
-  for (int i0 = 0; i0 < np; i0 += GROUP) {
-    float vals[GROUP][PER_LANE];
-    float mis[GROUP];
-#pragma unroll
-    for (int u = 0; u < GROUP; ++u) {
-      const int i = min(i0 + u, np - 1);
-      mis[u] = ml[2 * i];
-#pragma unroll
-      for (int c = 0; c < PER_LANE; ++c) vals[u][c] = acc[static_cast<int64_t>(i) * D + lane + c * kWave];
-    }
-#pragma unroll
-    for (int u = 0; u < GROUP; ++u) {
-      const float f = (i0 + u < np && mis[u] != neg_inf) ? fast_exp2(mis[u] - M) : 0.0f;
-#pragma unroll
-      for (int c = 0; c < PER_LANE; ++c) A[c] = fmaf(vals[u][c], f, A[c]);
-    }
-  }
-  const float inv = 1.0f / L;
-#pragma unroll
-  for (int c = 0; c < PER_LANE; ++c) p.out[row * D + lane + c * kWave] = E::store(A[c] * inv);
+  __syncthreads();
+  if (s_last == 0) return;
+  if (wave < heads_here) merge_partitions<E, D, true>(p, q_row0 + wave, np, lane);  // GC <= kWaves
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -963,12 +1040,23 @@ int64_t partitions_for(const Shape& s) {
   return (s.max_blocks * s.block_size + s.partition - 1) / s.partition;
 }
 
+// Workspace layout: partition accumulators (fp32, padded to 256 B), then partition (max, sum) pairs.
+size_t acc_bytes_for(const Shape& s) {
+  const size_t records = static_cast<size_t>(s.batch) * s.query_heads * s.num_partitions;
+  return (records * s.head_dim * sizeof(float) + 255) & ~size_t{255};
+}
+
 size_t workspace_for(const Shape& s) {
   if (s.num_partitions <= 1) return 0;
   const size_t records = static_cast<size_t>(s.batch) * s.query_heads * s.num_partitions;
-  const size_t acc = records * s.head_dim * sizeof(float);
-  const size_t acc_padded = (acc + 255) & ~size_t{255};
-  return acc_padded + records * 2 * sizeof(float);
+  return acc_bytes_for(s) + records * 2 * sizeof(float);
+}
+
+// Arrival counters of the fused launch: one 32-bit word per (sequence, KV head, head chunk).
+int64_t counter_words_for(int64_t batch, int64_t query_heads, int64_t kv_heads) {
+  const int64_t group = query_heads / kv_heads;
+  const int64_t gc = group == 1 ? 1 : (group == 2 ? 2 : 4);
+  return batch * kv_heads * ((group + gc - 1) / gc);
 }
 
 template <class E, int D, int GC, bool QK_MFMA>
@@ -1035,17 +1123,30 @@ extern "C" int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, 
   return RK_OK;
 }
 
+extern "C" int rk_pa_decode_counter_words(int64_t batch, int64_t query_heads, int64_t kv_heads,
+                                          size_t* words) {
+  if (words == nullptr) return fail(RK_ERR_INVALID_ARGUMENT, "words must not be NULL");
+  if (batch <= 0 || query_heads <= 0 || kv_heads <= 0)
+    return fail(RK_ERR_INVALID_ARGUMENT, "tensor dimensions must be positive");
+  if (query_heads % kv_heads != 0)
+    return fail(RK_ERR_INVALID_ARGUMENT, "query_heads must be divisible by kv_heads");
+  *words = static_cast<size_t>(counter_words_for(batch, query_heads, kv_heads));
+  return RK_OK;
+}
+
 namespace {
 
 constexpr int kPhasePartitions = 1;
 constexpr int kPhaseReduce = 2;
+constexpr int kPhaseFused = 4;  // partition kernel merging in its last workgroups; no reduce launch
 
 int decode_phases(const void* query, const void* key_cache, const void* value_cache,
                   const void* block_tables, const void* context_lengths, void* output, void* workspace,
                   size_t workspace_bytes, int64_t batch, int64_t query_heads, int64_t kv_heads,
                   int64_t head_dim, int64_t num_blocks, int64_t block_size,
                   int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
-                  int64_t partition_tokens, int variant, void* stream, int phases) {
+                  int64_t partition_tokens, int variant, void* stream, int phases,
+                  uint32_t* counters = nullptr, size_t counter_words = 0) {
   if (!query || !key_cache || !value_cache || !block_tables || !context_lengths || !output)
     return fail(RK_ERR_INVALID_ARGUMENT, "tensor pointers must not be NULL");
   if (dtype != RK_DTYPE_FP16 && dtype != RK_DTYPE_BF16)
@@ -1070,6 +1171,15 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
                 workspace_bytes);
   if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(RK_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  // The fused launch needs its counters only when some sequence can span several partitions.
+  const bool fused = (phases & kPhaseFused) != 0 && need > 0;
+  if (fused) {
+    const size_t words = static_cast<size_t>(counter_words_for(batch, query_heads, kv_heads));
+    if (counters == nullptr || counter_words < words)
+      return fail(RK_ERR_WORKSPACE, "%zu arrival counters required, %zu given", words, counter_words);
+    if ((reinterpret_cast<uintptr_t>(counters) & 3u) != 0)
+      return fail(RK_ERR_WORKSPACE, "counters must be 4-byte aligned");
+  }
 
   const int64_t group = query_heads / kv_heads;
   const int gc = head_chunk_for(group);
@@ -1090,11 +1200,10 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.context_lengths = context_lengths;
   prm.out = static_cast<uint16_t*>(output);
   if (need > 0) {
-    const size_t records = static_cast<size_t>(batch) * query_heads * s.num_partitions;
-    const size_t acc_bytes = (records * head_dim * sizeof(float) + 255) & ~size_t{255};
     prm.ws_acc = static_cast<float*>(workspace);
-    prm.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
+    prm.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes_for(s));
   }
+  prm.counters = fused ? counters : nullptr;
   prm.block_stride = block_size * kv_heads * head_dim;
   prm.row_stride = kv_heads * head_dim;
   prm.batch = static_cast<int32_t>(batch);
@@ -1111,8 +1220,8 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.index_is64 = index_dtype == RK_INDEX_INT64 ? 1 : 0;
   prm.scale_log2e = scale * kLog2e;
 
-  const bool partitions = (phases & kPhasePartitions) != 0;
-  const bool reduce = (phases & kPhaseReduce) != 0 && s.num_partitions > 1;
+  const bool partitions = (phases & (kPhasePartitions | kPhaseFused)) != 0;
+  const bool reduce = !fused && (phases & kPhaseReduce) != 0 && s.num_partitions > 1;
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const hipError_t err =
       dtype == RK_DTYPE_BF16
@@ -1164,6 +1273,20 @@ extern "C" int rk_pa_decode_reduce(const void* query, const void* key_cache,
                        workspace, workspace_bytes, batch, query_heads, kv_heads, head_dim,
                        num_blocks, block_size, max_blocks_per_sequence, scale, dtype, index_dtype,
                        partition_tokens, variant, stream, kPhaseReduce);
+}
+
+extern "C" int rk_pa_decode_fused(const void* query, const void* key_cache, const void* value_cache,
+                                  const void* block_tables, const void* context_lengths, void* output,
+                                  void* workspace, size_t workspace_bytes, uint32_t* counters,
+                                  size_t counter_words, int64_t batch, int64_t query_heads,
+                                  int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
+                                  int64_t block_size, int64_t max_blocks_per_sequence, float scale,
+                                  int dtype, int index_dtype, int64_t partition_tokens, int variant,
+                                  void* stream) {
+  return decode_phases(query, key_cache, value_cache, block_tables, context_lengths, output,
+                       workspace, workspace_bytes, batch, query_heads, kv_heads, head_dim,
+                       num_blocks, block_size, max_blocks_per_sequence, scale, dtype, index_dtype,
+                       partition_tokens, variant, stream, kPhaseFused, counters, counter_words);
 }
 
 extern "C" const char* rk_pa_last_error(void) { return g_last_error.c_str(); }

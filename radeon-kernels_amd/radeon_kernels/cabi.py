@@ -2,7 +2,8 @@
 
 This is the boundary a non-Python host (or a test) uses: plain device pointers, int64 sizes and a
 HIP stream handle.  ``decode`` adapts torch tensors to it (allocating the output and split-K
-workspace with torch on the current stream).  Loading fails loudly if the library was not built;
+workspace with torch on the current stream).  ``phase="fused"`` calls the single-launch entry,
+whose arrival counters the caller keeps zeroed (they are left zero by every completed call).  Loading fails loudly if the library was not built;
 there is no fallback here.
 
 torch is imported before the library is opened so that the library binds to the HIP runtime torch
@@ -33,6 +34,8 @@ EXPORTED_SYMBOLS = (
     "rk_pa_decode",
     "rk_pa_decode_partitions",
     "rk_pa_decode_reduce",
+    "rk_pa_decode_fused",
+    "rk_pa_decode_counter_words",
     "rk_pa_decode_workspace_bytes",
     "rk_pa_last_error",
     "rk_pa_version",
@@ -64,6 +67,10 @@ class PagedAttentionLibrary:
         for symbol in PHASES.values():
             getattr(lib, symbol).argtypes = decode_args
             getattr(lib, symbol).restype = ctypes.c_int
+        lib.rk_pa_decode_fused.argtypes = decode_args[:8] + [vp, sz] + decode_args[8:]
+        lib.rk_pa_decode_fused.restype = ctypes.c_int
+        lib.rk_pa_decode_counter_words.argtypes = [i64, i64, i64, ctypes.POINTER(sz)]
+        lib.rk_pa_decode_counter_words.restype = ctypes.c_int
         lib.rk_pa_last_error.argtypes = []
         lib.rk_pa_last_error.restype = ctypes.c_char_p
         lib.rk_pa_version.argtypes = []
@@ -87,20 +94,33 @@ class PagedAttentionLibrary:
                                                          partition_tokens, ctypes.byref(out)))
         return int(out.value)
 
+    def counter_words(self, batch: int, query_heads: int, kv_heads: int) -> int:
+        out = ctypes.c_size_t(0)
+        self.check(self.lib.rk_pa_decode_counter_words(batch, query_heads, kv_heads, ctypes.byref(out)))
+        return int(out.value)
+
     def decode_raw(self, *, query: int, key_cache: int, value_cache: int, block_tables: int, context_lengths: int,
                    output: int, workspace: int, workspace_bytes: int, batch: int, query_heads: int, kv_heads: int,
                    head_dim: int, num_blocks: int, block_size: int, max_blocks: int, scale: float, dtype: int,
-                   index_dtype: int, partition_tokens: int, variant: int, stream: int, phase: str = "all") -> int:
-        return getattr(self.lib, PHASES[phase])(query, key_cache, value_cache, block_tables, context_lengths, output,
-                                     workspace or None, workspace_bytes, batch, query_heads, kv_heads, head_dim,
-                                     num_blocks, block_size, max_blocks, ctypes.c_float(scale), dtype, index_dtype,
-                                     partition_tokens, variant, stream or None)
+                   index_dtype: int, partition_tokens: int, variant: int, stream: int, phase: str = "all",
+                   counters: int = 0, counter_words: int = 0) -> int:
+        head = (query, key_cache, value_cache, block_tables, context_lengths, output, workspace or None,
+                workspace_bytes)
+        tail = (batch, query_heads, kv_heads, head_dim, num_blocks, block_size, max_blocks, ctypes.c_float(scale),
+                dtype, index_dtype, partition_tokens, variant, stream or None)
+        if phase == "fused":
+            return self.lib.rk_pa_decode_fused(*head, counters or None, counter_words, *tail)
+        return getattr(self.lib, PHASES[phase])(*head, *tail)
 
     def decode(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
                scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
                out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
-               phase: str = "all") -> Any:
-        """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None)."""
+               phase: str = "all", counters: Any | None = None) -> Any:
+        """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None).
+
+        ``counters`` (phase ``"fused"`` only): an int32 tensor of at least ``counter_words`` zeros,
+        allocated zeroed here if None.
+        """
 
         import torch
 
@@ -116,6 +136,9 @@ class PagedAttentionLibrary:
             workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
         if stream is None:
             stream = torch.cuda.current_stream(query.device)
+        if phase == "fused" and counters is None:
+            counters = torch.zeros(self.counter_words(batch, query_heads, kv_heads), dtype=torch.int32,
+                                   device=query.device)
         status = self.decode_raw(
             query=query.data_ptr(), key_cache=key_cache.data_ptr(), value_cache=value_cache.data_ptr(),
             block_tables=block_tables.data_ptr(), context_lengths=context_lengths.data_ptr(), output=out.data_ptr(),
@@ -125,6 +148,8 @@ class PagedAttentionLibrary:
             dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
             index_dtype=RK_INDEX_INT64 if block_tables.dtype == torch.int64 else RK_INDEX_INT32,
             partition_tokens=partition_tokens, variant=VARIANTS[variant], stream=stream.cuda_stream, phase=phase,
+            counters=counters.data_ptr() if counters is not None else 0,
+            counter_words=counters.numel() if counters is not None else 0,
         )
         self.check(status)
         return out

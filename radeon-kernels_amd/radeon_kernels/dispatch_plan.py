@@ -8,8 +8,12 @@ regions get which entrypoint and launch parameters -- is this table.
 Operators and regions:
 
 * ``paged_attention_decode``: one exact entry (priority 100) per measured workload shape, with the
-  partition size chosen for that shape (``launch.partition_tokens``), and one broad gfx950 region
-  (priority 10) covering every shape the library accepts;
+  partition size chosen for that shape (``launch.partition_tokens``) and how its partition records
+  are merged (``launch.merge``: ``fused`` -- the partition kernel's last workgroup per sequence and
+  head slot merges, one launch -- measured 7-12% faster on the 256-workgroup shapes; ``reduce`` -- a
+  separate reduce launch, 0.5% faster on the 8192-workgroup ragged batch), and one broad gfx950
+  region (priority 10) covering every shape the library accepts with ``merge: auto`` (fused below
+  4096 workgroups);
 * ``kv_cache_append`` and ``kv_cache_copy``: one exact entry per case of the reference's workload files
   (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18, kv_cache_copy-1.0.yaml:12-17) and one broad
   gfx950 region each; their bindings (entrypoints ``append`` and ``copy``) share one kernel library.
@@ -49,31 +53,31 @@ EXACT_REGIONS: list[tuple[str, dict[str, Any], dict[str, Any]]] = [
         "b1-gqa32x8-c128-d128-p16-fp16",
         {"dtype": "fp16", "batch": 1, "query_heads": 32, "kv_heads": 8, "head_dim": 128, "num_blocks": 64,
          "block_size": 16, "max_blocks_per_sequence": 8},
-        {"partition_tokens": 128},
+        {"partition_tokens": 128, "merge": "fused"},
     ),
     (
         "b8-gqa32x8-c1024-d128-p16-bf16",
         {"dtype": "bf16", "batch": 8, "query_heads": 32, "kv_heads": 8, "head_dim": 128, "num_blocks": 1024,
          "block_size": 16, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 256},
+        {"partition_tokens": 256, "merge": "fused"},
     ),
     (
         "b4-mha16-c2048-d64-p32-bf16",
         {"dtype": "bf16", "batch": 4, "query_heads": 16, "kv_heads": 16, "head_dim": 64, "num_blocks": 512,
          "block_size": 32, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 512},
+        {"partition_tokens": 512, "merge": "fused"},
     ),
     (
         "b4-gqa32x8-c1024-d256-p16-fp16",
         {"dtype": "fp16", "batch": 4, "query_heads": 32, "kv_heads": 8, "head_dim": 256, "num_blocks": 512,
          "block_size": 16, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 128},
+        {"partition_tokens": 128, "merge": "fused"},
     ),
     (
         "b128-gqa32x8-ragged-d128-p16-bf16",
         {"dtype": "bf16", "batch": 128, "query_heads": 32, "kv_heads": 8, "head_dim": 128,
          "num_blocks": [1, _INT_MAX], "block_size": 16, "max_blocks_per_sequence": 1024},
-        {"partition_tokens": 2048},
+        {"partition_tokens": 2048, "merge": "reduce"},
     ),
 ]
 
@@ -87,7 +91,7 @@ BROAD_REGION: dict[str, Any] = {
     "block_size": {"one_of": _POW2_BLOCKS},
     "max_blocks_per_sequence": [1, _INT_MAX],
 }
-BROAD_LAUNCH = {"partition_tokens": 256}
+BROAD_LAUNCH = {"partition_tokens": 256, "merge": "auto"}
 
 _COMMON = {
     "index_dtype": {"one_of": ["int32", "int64"]},

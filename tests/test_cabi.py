@@ -130,6 +130,39 @@ def test_phase_entry_points_validate_identically(lib):
         assert status == cabi.RK_ERR_INVALID_ARGUMENT and "NULL" in lib.last_error()
 
 
+def test_counter_words_formula(lib):
+    """One arrival counter per (sequence, KV head, head chunk); chunks hold 1, 2 or 4 query heads."""
+
+    for batch, hq, hkv, expected in [(128, 32, 8, 128 * 8), (3, 64, 8, 3 * 8 * 2), (2, 12, 4, 2 * 4),
+                                     (5, 8, 8, 40), (1, 16, 8, 8), (2, 40, 8, 2 * 8 * 2)]:
+        assert lib.counter_words(batch, hq, hkv) == expected
+    out = ctypes.c_size_t(0)
+    assert lib.lib.rk_pa_decode_counter_words(1, 8, 2, None) == cabi.RK_ERR_INVALID_ARGUMENT
+    assert lib.lib.rk_pa_decode_counter_words(1, 9, 2, ctypes.byref(out)) == cabi.RK_ERR_INVALID_ARGUMENT
+    assert lib.lib.rk_pa_decode_counter_words(0, 8, 2, ctypes.byref(out)) == cabi.RK_ERR_INVALID_ARGUMENT
+
+
+@cpu_only
+@pytest.mark.parametrize(
+    "overrides, status, message",
+    [
+        (dict(counters=0, counter_words=0), cabi.RK_ERR_WORKSPACE, "arrival counters required"),
+        (dict(counters=4096, counter_words=3), cabi.RK_ERR_WORKSPACE, "4 arrival counters required, 3 given"),
+        (dict(counters=4098, counter_words=64), cabi.RK_ERR_WORKSPACE, "4-byte aligned"),
+        (dict(query=0), cabi.RK_ERR_INVALID_ARGUMENT, "must not be NULL"),
+        (dict(workspace=0, workspace_bytes=0), cabi.RK_ERR_WORKSPACE, "workspace of"),
+    ],
+)
+def test_fused_entry_validates_counters_before_launch(lib, overrides, status, message):
+    # batch 2, 8 query heads over 2 KV heads (one chunk of 4) -> 4 counters; 4 partitions of 64 tokens.
+    args = dict(phase="fused", max_blocks=16, workspace=1 << 20, workspace_bytes=1 << 20, counters=4096,
+                counter_words=64)
+    args.update(overrides)
+    got, text = call(lib, **args)
+    assert got == status, text
+    assert message in text
+
+
 @cpu_only
 def test_last_error_is_per_thread(lib):
     import threading

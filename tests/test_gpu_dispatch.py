@@ -63,7 +63,7 @@ def test_public_api_ragged_b128_selects_exact_entry(gpu):
     record = rk.get_last_dispatch()
     assert record["selected"] == "native/decode_mfma"
     assert record["entry_id"] == "paged_attention_decode-gfx950-b128-gqa32x8-ragged-d128-p16-bf16"
-    assert record["launch"] == {"partition_tokens": 2048}
+    assert record["launch"] == {"partition_tokens": 2048, "merge": "reduce"}
     assert torch.isfinite(out).all().item()
     del data
     torch.cuda.empty_cache()
@@ -132,3 +132,64 @@ def test_graph_capture_replays_match_eager(gpu):
         torch.cuda.synchronize()
         assert torch.equal(captured, eager)
         del scratch
+
+
+def _binding():
+    import importlib.util
+
+    from radeon_kernels.cabi import LIBRARY_PATH
+
+    path = LIBRARY_PATH.parent / "rk_pa_gfx950.so"
+    spec = importlib.util.spec_from_file_location("rk_pa_gfx950", path)
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
+def test_binding_merge_forms_agree_bit_for_bit(gpu):
+    """The binding's ``merge`` launch parameter: fused, reduce and auto give identical outputs."""
+
+    import torch
+
+    binding = _binding()
+    case = make_case(torch, batch=6, query_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                     contexts=[1, 300, 1024, 2047, 4000, 77], dtype="bf16", seed=31)
+    dev = to_device(case, gpu)
+    args = (dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"], dev["context_lengths"], 0.088)
+    announce("binding merge forms")
+    outs = {merge: binding.decode_mfma(*args, partition_tokens=256, merge=merge) for merge in ("reduce", "fused", "auto")}
+    outs["valu-fused"] = binding.decode_valu(*args, partition_tokens=256, merge="fused")
+    outs["valu-reduce"] = binding.decode_valu(*args, partition_tokens=256, merge="reduce")
+    torch.cuda.synchronize()
+    assert torch.equal(outs["fused"], outs["reduce"]) and torch.equal(outs["auto"], outs["reduce"])
+    assert torch.equal(outs["valu-fused"], outs["valu-reduce"])
+    assert_within(outs["fused"], oracle64(case, scale=0.088), "bf16", "binding fused")
+    with pytest.raises(ValueError, match="merge must be"):
+        binding.decode_mfma(*args, partition_tokens=256, merge="tree")
+
+
+def test_fused_calls_on_two_streams_use_separate_counters(gpu):
+    """Fused calls in flight on two streams at once: each stream has its own counter buffer, so
+    both match their single-stream results on every repetition."""
+
+    import torch
+
+    binding = _binding()
+    cases = [make_case(torch, batch=8, query_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                       contexts=[900 + 150 * i for i in range(8)], dtype="bf16", seed=40 + s) for s in range(2)]
+    devs = [to_device(c, gpu) for c in cases]
+    argss = [(d["query"], d["key_cache"], d["value_cache"], d["block_tables"], d["context_lengths"], 0.088) for d in devs]
+    announce("fused on two streams")
+    expected = [binding.decode_mfma(*a, partition_tokens=128, merge="reduce") for a in argss]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    results = [[], []]
+    for _ in range(20):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                results[i].append(binding.decode_mfma(*argss[i], partition_tokens=128, merge="fused"))
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert all(torch.equal(r, expected[i]) for r in results[i]), f"stream {i}"

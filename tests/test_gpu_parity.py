@@ -188,3 +188,86 @@ def test_deterministic(gpu, palib):
     runs = [palib.decode(data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
                          data["context_lengths"], partition_tokens=64) for _ in range(3)]
     assert all(torch.equal(runs[0], r) for r in runs[1:])
+
+
+# ---------------------------------------------------------------------------------------------
+# Single-launch form (rk_pa_decode_fused): the partition kernel's last workgroup per (sequence,
+# head slot) merges the records with the reduce kernel's own merge code, so it must agree with
+# the two-launch form bit for bit, and leave its arrival counters zero after every call.
+def _fused_vs_two_launch(palib, dev, partition, counters, variant="mfma"):
+    import torch
+
+    args = (dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"], dev["context_lengths"])
+    two = palib.decode(*args, partition_tokens=partition, variant=variant)
+    fused = palib.decode(*args, partition_tokens=partition, variant=variant, phase="fused", counters=counters)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), two.view(torch.int16)), "fused and two-launch outputs differ"
+    assert int(counters.abs().sum().item()) == 0, "arrival counters not left zero"
+    return fused
+
+
+@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("key", ["c1", "c2", "c3", "c4"])
+def test_fused_matches_two_launch_on_measured_workloads(gpu, palib, key, variant):
+    import torch
+    from radeon_kernels.workloads import make_inputs
+
+    data = make_inputs(key)
+    dev = to_device(data, gpu)
+    announce(f"fused {key} variant={variant}")
+    counters = torch.zeros(1 << 16, dtype=torch.int32, device=gpu)
+    out = _fused_vs_two_launch(palib, dev, WORKLOAD_PARTITIONS[key], counters, variant)
+    assert_within(out, oracle64(data), data["workload"].dtype, f"fused {key}/{variant} vs float64 oracle")
+
+
+@pytest.mark.parametrize("partition", [16, 64, 1024])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_fused_shape_sweep(gpu, palib, shape, partition):
+    import torch
+
+    hq, hkv, d, bs, dtype = shape
+    if partition // bs > 256:
+        pytest.skip("partition_tokens / block_size must be <= 256")
+    case = make_case(torch, batch=3, query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bs,
+                     contexts=[5, bs * 3 + 1, 1500], dtype=dtype, seed=hq * 5 + d + bs)
+    dev = to_device(case, gpu)
+    announce(f"fused shape {shape} partition={partition}")
+    counters = torch.zeros(palib.counter_words(3, hq, hkv), dtype=torch.int32, device=gpu)
+    out = _fused_vs_two_launch(palib, dev, partition, counters)
+    assert_within(out, oracle64(case), dtype, f"fused shape {shape}")
+
+
+def test_fused_counters_serve_consecutive_calls_of_different_shapes(gpu, palib):
+    """One counter buffer, stream-ordered calls: a large batch, then a smaller one, then empty and
+    over-long contexts, then the large batch again.  Each must match the two-launch form."""
+
+    import torch
+
+    counters = torch.zeros(4096, dtype=torch.int32, device=gpu)
+    cases = [
+        make_case(torch, batch=16, query_heads=32, kv_heads=8, head_dim=128, block_size=16,
+                  contexts=[37 * i + 900 for i in range(16)], dtype="bf16", seed=21),
+        make_case(torch, batch=3, query_heads=8, kv_heads=2, head_dim=64, block_size=16,
+                  contexts=[700, 12, 333], dtype="fp16", seed=22),
+        make_case(torch, batch=4, query_heads=8, kv_heads=2, head_dim=128, block_size=16,
+                  contexts=[0, 90, -1, 200], max_blocks=8, dtype="fp16", seed=23),
+    ]
+    for round_ in range(2):
+        for i, case in enumerate(cases):
+            dev = to_device(case, gpu)
+            announce(f"fused consecutive round {round_} case {i}")
+            out = _fused_vs_two_launch(palib, dev, 64, counters)
+            assert_within(out, oracle64(case), case["dtype"], f"consecutive case {i}")
+
+
+def test_fused_ragged_b128_matches_two_launch(gpu, palib):
+    import torch
+    from radeon_kernels.workloads import make_inputs
+
+    announce("fused c5 ragged b128")
+    data = make_inputs("c5", device=gpu, generator_device=gpu)
+    counters = torch.zeros(palib.counter_words(128, 32, 8), dtype=torch.int32, device=gpu)
+    for _ in range(2):
+        _fused_vs_two_launch(palib, data, 2048, counters)
+    del data
+    torch.cuda.empty_cache()

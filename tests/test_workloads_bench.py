@@ -87,6 +87,10 @@ def test_bench_reads_traffic_only_for_its_exact_configuration(tmp_path, monkeypa
     assert bench.read_traffic("b128-x", "mfma", 2048) == 4_867_000_000
     assert bench.read_traffic("b128-x", "mfma", 1024) is None
     assert bench.read_traffic("other", "mfma", 2048) is None
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused") is None  # measured in the reduce form
+    summary.write_text(summary.read_text() + "merge = fused\n")
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused") == 4_867_000_000
+    assert bench.read_traffic("b128-x", "mfma", 2048) is None
     monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", tmp_path / "absent.txt")
     assert bench.read_traffic("b128-x", "mfma", 2048) is None
 
@@ -95,9 +99,10 @@ def test_bench_uses_the_dispatch_table_launch():
     import bench
     from radeon_kernels import dispatch_plan
 
-    entrypoint, partition = bench.dispatch_launch("c5")
+    entrypoint, partition, merge = bench.dispatch_launch("c5")
     assert entrypoint == dispatch_plan.ENTRYPOINT
-    assert {"partition_tokens": partition} == [launch for suffix, _, launch in dispatch_plan.EXACT_REGIONS
-                                               if suffix.startswith("b128")][0]
+    assert {"partition_tokens": partition, "merge": merge} == [
+        launch for suffix, _, launch in dispatch_plan.EXACT_REGIONS if suffix.startswith("b128")][0]
+    assert [bench.dispatch_launch(key)[2] for key in ("c1", "c2", "c3", "c4", "c5")] == ["fused"] * 4 + ["reduce"]
     args = bench.parse_args([])
     assert (args.gpus, args.workload) == (1, "c5")

@@ -10,12 +10,12 @@ Outputs (all under ``radeon-kernels_amd/packs/gfx950``):
 * ``manifest.json``          -- the kernel-pack manifest (same fields as the reference's
   ``schemas/kernel-pack.schema.json``), stamped with the bindings' SHA-256 and this environment.
 
-Dispatch entries load the bindings as ``python_extension`` artifacts; each binding carries the
-SHA-256 of the library it links and refuses to import against any other.  The build also rewrites
-the winners' ``sha256`` and ``environment`` in ``radeon_kernels/dispatch/<operator>-1.0.json`` from
-``dispatch_plan.py``.  The
-reference binds every dispatch entry to the exact artifact digest and to the exact
-torch/Python/ROCm ABI (src/radeon_kernels/runtime/compatibility.py:94-102), so both files are
+Each HIP source is compiled once and linked into both its C-ABI library and its bindings, so a
+binding depends on no other file of the pack and the digest a dispatch entry pins covers the
+kernels the binding runs.  The build also rewrites the winners' ``sha256`` and ``environment`` in
+``radeon_kernels/dispatch/<operator>-1.0.json`` from ``dispatch_plan.py``.  The reference binds every
+dispatch entry to the exact artifact digest and to the exact torch/Python/ROCm ABI
+(src/radeon_kernels/runtime/compatibility.py:94-102), so both files are
 generated after each build rather than written by hand.
 
 Run as ``python radeon-kernels_amd/build.py`` or through ``__graft_entry__.build()``.
@@ -47,7 +47,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # Packed-FP32 VALU ops stay disabled: all fp32 math uses the scalar VALU forms.
     "-Xclang",
     "-target-feature",
@@ -108,25 +107,27 @@ def sha256_file(path: Path) -> str:
 
 
 class Library:
-    """One C-ABI kernel library (hipcc) plus the torch binding modules (g++) that link against it.
+    """One HIP source compiled once (hipcc -c) and linked twice: into the C-ABI kernel library
+    (hipcc -shared) and into each torch binding module (g++), so that every binding is
+    self-contained -- a pack then consists of its manifest, its signature and the artifacts the
+    manifest names, the release layout the reference's installer accepts (installer.py:187-220),
+    and an artifact's digest covers the kernels it runs.
 
     ``bindings`` maps each binding module name to the operators whose dispatch entries name it; a
-    pack needs one artifact file per operator, so operators sharing a library get one module each,
+    pack needs one artifact file per operator, so operators sharing a source get one module each,
     all built from the same binding source."""
 
-    def __init__(self, hip_source: str, cabi_name: str, binding_source: str, digest_symbol: str,
+    def __init__(self, hip_source: str, cabi_name: str, binding_source: str,
                  bindings: dict[str, tuple[str, ...]]) -> None:
         self.hip_source = CSRC / hip_source
         self.cabi_name = cabi_name
         self.binding_source = CSRC / binding_source
-        self.digest_symbol = digest_symbol
         self.bindings = bindings
 
 
 LIBRARIES = (
-    Library("pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", "kRkKernelLibrarySha256",
-            {EXTENSION_NAME: ("paged_attention_decode",)}),
-    Library("kv_cache_gfx950.hip", "librk_kv_gfx950.so", "kv_torch_ext.cpp", "kRkKvLibrarySha256",
+    Library("pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", {EXTENSION_NAME: ("paged_attention_decode",)}),
+    Library("kv_cache_gfx950.hip", "librk_kv_gfx950.so", "kv_torch_ext.cpp",
             {"rk_kv_append_gfx950": ("kv_cache_append",), "rk_kv_copy_gfx950": ("kv_cache_copy",)}),
 )
 
@@ -144,11 +145,13 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
     includes, libraries = _torch_paths()
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
 
-    # All compilations run concurrently; each binding is linked once its library exists.
+    # All compilations run concurrently; the library and the bindings are linked once the kernel
+    # object exists.
     jobs = []
     for lib in LIBRARIES:
-        cabi_tmp = work / lib.cabi_name
-        hip = _run([_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(lib.hip_source), "-o", str(cabi_tmp)], verbose)
+        kernel_obj = work / f"{lib.hip_source.stem}.o"
+        hip = _run([_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(lib.hip_source), "-o", str(kernel_obj)],
+                   verbose)
         objects = {}
         for module in lib.bindings:
             ext_obj = work / f"{module}.o"
@@ -172,17 +175,15 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
                 str(ext_obj),
             ]
             objects[module] = (ext_obj, _run(cxx, verbose))
-        jobs.append((lib, cabi_tmp, hip, objects))
+        jobs.append((lib, kernel_obj, hip, objects))
 
+    rocm_lib = str(Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib")
     bindings: dict[str, Path] = {}
-    for lib, cabi_tmp, hip, objects in jobs:
-        _finish(hip, f"hipcc ({lib.cabi_name})")
-        # The bindings check at import that the kernel library they load is the one built here.
-        digest_src = work / f"{lib.cabi_name}.digest.cpp"
-        digest_obj = work / f"{lib.cabi_name}.digest.o"
-        digest_src.write_text(f'extern const char {lib.digest_symbol}[] = "{sha256_file(cabi_tmp)}";\n')
-        _finish(_run(["g++", "-O2", "-fPIC", "-c", str(digest_src), "-o", str(digest_obj)], verbose),
-                f"g++ ({lib.cabi_name} digest)")
+    for lib, kernel_obj, hip, objects in jobs:
+        _finish(hip, f"hipcc ({lib.hip_source.name})")
+        cabi_tmp = work / lib.cabi_name
+        _finish(_run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(kernel_obj), "-Wl,--build-id=none",
+                      "-o", str(cabi_tmp)], verbose), f"hipcc link ({lib.cabi_name})")
         linked = []
         for module, (ext_obj, gxx) in objects.items():
             _finish(gxx, f"g++ ({module} binding)")
@@ -191,17 +192,16 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
                 "g++",
                 "-shared",
                 str(ext_obj),
-                str(digest_obj),
-                f"-L{work}",
+                str(kernel_obj),
                 *[f"-L{path}" for path in libraries],
-                "-l:" + lib.cabi_name,
+                f"-L{rocm_lib}",
+                "-lamdhip64",
                 "-lc10",
                 "-lc10_hip",
                 "-ltorch",
                 "-ltorch_cpu",
                 "-ltorch_hip",
                 "-ltorch_python",
-                "-Wl,-rpath,$ORIGIN",
                 "-Wl,--build-id=none",
                 "-o",
                 str(ext_tmp),
@@ -214,7 +214,7 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
             ext_obj.unlink()
             for operator in lib.bindings[module]:
                 bindings[operator] = LIB_DIR / f"{module}.so"
-        digest_obj.unlink()
+        kernel_obj.unlink()
     return bindings
 
 
@@ -254,6 +254,12 @@ def write_pack_and_dispatch(bindings: dict[str, Path]) -> dict:
 
 def build(verbose: bool = False) -> dict:
     summary = write_pack_and_dispatch(compile_libraries(verbose=verbose))
+    # Sign the pack manifest (the runtime loads only signed packs) and rewrite the promotion records
+    # from the committed GPU evaluations (promotion/publish.py).
+    sys.path.insert(0, str(PACKAGE_ROOT / "promotion"))
+    from publish import publish
+
+    summary["promotion"] = publish()
     if verbose:
         print(json.dumps(summary, indent=2), flush=True)
     return summary

@@ -8,10 +8,8 @@
 // block_mapping)): they validate, write the caches in place on the current HIP stream and return
 // them.  No host synchronisation, no device-to-host reads: safe under HIP graph capture.
 //
-// The kernels live in librk_kv_gfx950.so next to this module.  The build bakes that library's
-// SHA-256 into this module and the import fails unless the library actually loaded has it, so the
-// digest a dispatch entry pins for this module also pins the kernels it runs.
-#include <dlfcn.h>
+// The kernels (kv_cache_gfx950.hip) are linked into this module, so it depends on no other file of
+// the pack and the digest a dispatch entry pins for it covers the kernels it runs.
 #include <torch/extension.h>
 
 #include <c10/hip/HIPStream.h>
@@ -21,20 +19,7 @@
 
 #include "rk_kv_cache.h"
 
-// Defined in a file the build generates after compiling the kernel library.
-extern const char kRkKvLibrarySha256[];
-
 namespace {
-
-std::string loaded_kernel_library_digest(std::string* path_out) {
-  Dl_info info{};
-  if (dladdr(reinterpret_cast<void*>(&rk_kv_version), &info) == 0 || info.dli_fname == nullptr) {
-    throw py::import_error("rk_kv: cannot locate the loaded kernel library");
-  }
-  *path_out = info.dli_fname;
-  py::bytes content = py::module_::import("pathlib").attr("Path")(*path_out).attr("read_bytes")();
-  return py::module_::import("hashlib").attr("sha256")(content).attr("hexdigest")().cast<std::string>();
-}
 
 void check_data(const at::Tensor& t, const char* name, int64_t rank) {
   TORCH_CHECK_VALUE(t.is_cuda(), name, " must be a ROCm tensor");
@@ -112,14 +97,6 @@ std::vector<at::Tensor> copy(at::Tensor key_cache, at::Tensor value_cache, const
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
   module.doc() = "gfx950 paged KV-cache append (row gather/scatter) and block copy";
-  std::string library_path;
-  const std::string digest = loaded_kernel_library_digest(&library_path);
-  if (digest != kRkKvLibrarySha256) {
-    throw py::import_error("rk_kv: kernel library " + library_path + " has SHA-256 " + digest +
-                           ", this module was built against " + kRkKvLibrarySha256);
-  }
-  module.attr("kernel_library") = library_path;
-  module.attr("kernel_library_sha256") = digest;
   module.def("append", &append, "append token K/V rows to their paged-cache slots", py::arg("key"),
              py::arg("value"), py::arg("key_cache"), py::arg("value_cache"), py::arg("slot_mapping"));
   module.def("copy", &copy, "copy whole cache blocks (source, destination pairs)", py::arg("key_cache"),

@@ -20,10 +20,8 @@
 // for the next call on that stream.  Calls made while the stream is being captured into a graph
 // always use the two-launch form, which needs no state that outlives the call.
 //
-// The kernels live in librk_pa_gfx950.so next to this module.  The build bakes that library's
-// SHA-256 into this module and the import fails unless the library actually loaded has it, so the
-// digest a dispatch entry pins for this module also pins the kernels it runs.
-#include <dlfcn.h>
+// The kernels (pa_decode_gfx950.hip) are linked into this module, so it depends on no other file
+// of the pack and the digest a dispatch entry pins for it covers the kernels it runs.
 #include <torch/extension.h>
 
 #include <c10/hip/HIPStream.h>
@@ -36,21 +34,7 @@
 
 #include "rk_paged_attention.h"
 
-// Defined in a file the build generates after compiling the kernel library.
-extern const char kRkKernelLibrarySha256[];
-
 namespace {
-
-// SHA-256 (hex) of the shared object that provides the C ABI in this process.
-std::string loaded_kernel_library_digest(std::string* path_out) {
-  Dl_info info{};
-  if (dladdr(reinterpret_cast<void*>(&rk_pa_version), &info) == 0 || info.dli_fname == nullptr) {
-    throw py::import_error("rk_pa_gfx950: cannot locate the loaded kernel library");
-  }
-  *path_out = info.dli_fname;
-  py::bytes content = py::module_::import("pathlib").attr("Path")(*path_out).attr("read_bytes")();
-  return py::module_::import("hashlib").attr("sha256")(content).attr("hexdigest")().cast<std::string>();
-}
 
 void check_data(const at::Tensor& t, const char* name, int64_t rank) {
   TORCH_CHECK_VALUE(t.is_cuda(), name, " must be a ROCm tensor");
@@ -206,14 +190,6 @@ at::Tensor decode_valu(const at::Tensor& query, const at::Tensor& key_cache,
 
 PYBIND11_MODULE(rk_pa_gfx950, module) {
   module.doc() = "gfx950 split-K paged-attention decode (MFMA QK^T or VALU QK^T, VALU PV)";
-  std::string library_path;
-  const std::string digest = loaded_kernel_library_digest(&library_path);
-  if (digest != kRkKernelLibrarySha256) {
-    throw py::import_error("rk_pa_gfx950: kernel library " + library_path + " has SHA-256 " + digest +
-                           ", this module was built against " + kRkKernelLibrarySha256);
-  }
-  module.attr("kernel_library") = library_path;
-  module.attr("kernel_library_sha256") = digest;
   module.def("decode_mfma", &decode_mfma, "paged decode, QK^T on MFMA", py::arg("query"),
              py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
              py::arg("context_lengths"), py::arg("scale"), py::kw_only(),

@@ -64,7 +64,7 @@ class OperatorRuntime:
         registry: DispatchRegistry | None = None,
         pack_roots: Iterable[Path] | None = None,
         pack_registry: KernelPackRegistry | None = None,
-        require_pack_signatures: bool = False,
+        require_pack_signatures: bool = True,
         loader_factory: Callable[[Path], PrecompiledArtifactLoader] = PrecompiledArtifactLoader,
         fingerprint_detector: Callable[..., EnvironmentFingerprint] = EnvironmentFingerprint.detect,
         strict_native: bool = False,

@@ -6,13 +6,14 @@ prefix; a root is either a pack itself (contains ``manifest.json``) or a directo
 invalid packs are collected as ``rejected`` rather than raised; ``resolve`` needs a pack whose
 environment matches the fingerprint and whose artifact record equals the dispatch winner exactly.
 
-Differences, both deliberate:
+Signatures are required by default, as in the reference (packs.py:88-113): every pack's
+``manifest.json`` must carry a ``manifest.sig.json`` that verifies under the trusted keyring
+(radeon_kernels.runtime.signing; the built-in keyring unless one is given), else the pack is
+rejected with the reason.
 
-* the in-tree pack directory written by the build (``radeon-kernels_amd/packs``) is appended as the
-  last default root, so a source checkout finds its own gfx950 pack without installation;
-* detached-signature verification is a hook.  The reference verifies Ed25519 signatures with a
-  release key this build does not hold; here ``require_signatures`` defaults to False and, when set,
-  needs a ``signature_verifier`` callable (packs are rejected without one).
+One deliberate difference: the in-tree pack directory written by the build
+(``radeon-kernels_amd/packs``) is appended as the last default root, so a source checkout finds its
+own gfx950 pack without installation.  The build signs that pack's manifest with its development key.
 """
 
 from __future__ import annotations
@@ -21,12 +22,18 @@ import os
 import sys
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Callable, Iterable, Mapping, Sequence
+from typing import Iterable, Mapping, Sequence
 
 from radeon_kernels.errors import ConfigError, RadeonKernelsError
 from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint
 from radeon_kernels.runtime.pack import KernelPack, KernelPackArtifact
 from radeon_kernels.runtime.registry import ArtifactSpec
+from radeon_kernels.runtime.signing import (
+    SignatureVerificationError,
+    TrustedKeyring,
+    builtin_trusted_keyring,
+    verify_detached_file,
+)
 
 PACK_PATH_ENVIRONMENT_VARIABLE = "RADEON_KERNELS_PACK_PATH"
 IN_TREE_PACK_ROOT = Path(__file__).resolve().parents[2] / "packs"
@@ -34,10 +41,6 @@ IN_TREE_PACK_ROOT = Path(__file__).resolve().parents[2] / "packs"
 
 class PackResolutionError(RadeonKernelsError):
     """No discovered pack can satisfy an approved dispatch entry."""
-
-
-class SignatureVerificationUnavailable(RadeonKernelsError):
-    """Signatures were required but no verifier is configured."""
 
 
 @dataclass(frozen=True)
@@ -94,21 +97,21 @@ class KernelPackRegistry:
         cls,
         roots: Iterable[Path],
         *,
-        require_signatures: bool = False,
-        signature_verifier: Callable[[Path], None] | None = None,
+        require_signatures: bool = True,
+        trusted_keys: TrustedKeyring | None = None,
     ) -> KernelPackRegistry:
         packs: list[KernelPack] = []
         rejected: list[str] = []
+        keyring = trusted_keys
+        if require_signatures and keyring is None:
+            keyring = builtin_trusted_keyring()
         for directory in pack_directories(roots):
             try:
                 if require_signatures:
-                    if signature_verifier is None:
-                        raise SignatureVerificationUnavailable(
-                            "pack signatures are required but no signature verifier is configured"
-                        )
-                    signature_verifier(directory)
+                    verify_detached_file(directory / "manifest.json", directory / "manifest.sig.json", keyring,
+                                         signed_file="manifest.json")
                 packs.append(KernelPack.from_directory(directory, verify_artifacts=False))
-            except (ConfigError, RadeonKernelsError) as error:
+            except (ConfigError, SignatureVerificationError, RadeonKernelsError) as error:
                 rejected.append(f"{directory}: {error}")
         return cls(packs, rejected=rejected)
 

@@ -15,6 +15,13 @@ Writes:
                    the reference's published dispatch manifests for these operators (data,
                    Apache-2.0), used to prove the gfx950 entries merge into them; copied from
                    /root/reference when that tree is present.
+  reference_signing/
+                   signature vectors for the Ed25519 verifier: the reference's trusted keyring
+                   (keys/trusted-keys.json), every detached signature envelope it publishes
+                   (evidence/, approvals/, pack-index/, compatibility/ *.sig.json) collected in
+                   signatures.json, three
+                   signed documents with their envelopes (one evidence record, one approval, the
+                   paged-attention pack-index record) and the JSON schemas of those record types.
 
 The reference repository holds no numeric vectors for this operator; these are produced by the
 oracle's brute force, which the tests pin independently (closed forms, library SDPA, invariants).
@@ -112,7 +119,38 @@ def main() -> None:
             document = json.loads(source.read_text(encoding="utf-8"))
             (HERE / f"reference_dispatch_{operator}-1.0.json").write_text(
                 json.dumps(document, indent=1, sort_keys=True) + "\n", encoding="utf-8")
+    write_signing_fixtures(Path("/root/reference"))
     print("fixtures written to", HERE)
+
+
+SIGNED_EXAMPLES = (
+    "evidence/m6-20260918-paged_attention_decode-gfx1201-b1-gqa32x8-c128-d128-p16-bf16",
+    "approvals/approval-proposal-m6-20260918-paged_attention_decode-gfx1201-b1-gqa32x8-c128-d128-p16-bf16-"
+    "3b9165d37c22d4c4-approved",
+    "pack-index/paged_attention_decode-1.0",
+)
+SCHEMAS = ("evidence", "approval", "pack-index", "signature", "trusted-keys", "kernel-pack", "dispatch")
+
+
+def write_signing_fixtures(reference: Path) -> None:
+    if not (reference / "keys" / "trusted-keys.json").is_file():
+        return
+    out = HERE / "reference_signing"
+    (out / "schemas").mkdir(parents=True, exist_ok=True)
+    (out / "trusted-keys.json").write_bytes((reference / "keys" / "trusted-keys.json").read_bytes())
+    envelopes = []
+    for directory in ("evidence", "approvals", "pack-index", "compatibility"):
+        for path in sorted((reference / directory).glob("*.sig.json")):
+            envelopes.append({"path": f"{directory}/{path.name}",
+                              "envelope": json.loads(path.read_text(encoding="utf-8"))})
+    (out / "signatures.json").write_text(json.dumps(envelopes, indent=0, sort_keys=True) + "\n", encoding="utf-8")
+    for stem in SIGNED_EXAMPLES:
+        for suffix in (".json", ".sig.json"):
+            source = reference / (stem + suffix)
+            (out / (Path(stem).name + suffix)).write_bytes(source.read_bytes())  # byte-exact: signed content
+    for name in SCHEMAS:
+        source = reference / "schemas" / f"{name}.schema.json"
+        (out / "schemas" / source.name).write_bytes(source.read_bytes())
 
 
 if __name__ == "__main__":

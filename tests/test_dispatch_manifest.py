@@ -149,41 +149,35 @@ def test_contract_document_matches_the_api():
     assert callable(getattr(importlib.import_module(module_name), function))
 
 
-def _binding_import_script(lib_dir: Path) -> str:
-    return (
-        "import sys, importlib.util\n"
-        "import torch\n"
-        f"spec = importlib.util.spec_from_file_location('rk_pa_gfx950', r'{lib_dir / 'rk_pa_gfx950.so'}')\n"
-        "module = importlib.util.module_from_spec(spec)\n"
-        "spec.loader.exec_module(module)\n"
-        "print(module.kernel_library_sha256)\n"
-    )
-
-
-def test_binding_pins_the_kernel_library_it_loads(tmp_path):
-    """The pack digest names the binding; the binding refuses a kernel library other than its own."""
+def _import_alone(tmp_path: Path, binary: Path, entrypoints: tuple[str, ...]):
+    """Import a binding copied alone into an empty directory (a fresh interpreter per call)."""
 
     import shutil
     import subprocess
     import sys
 
-    lib_dir = PACK / "lib"
-    if not (lib_dir / "rk_pa_gfx950.so").is_file():
+    if not binary.is_file():
         pytest.fail("the kernel pack is not built; run __graft_entry__.build()")
-    expected = hashlib.sha256((lib_dir / "librk_pa_gfx950.so").read_bytes()).hexdigest()
-    ok = subprocess.run([sys.executable, "-c", _binding_import_script(lib_dir)], capture_output=True, text=True,
-                        timeout=300)
-    assert ok.returncode == 0, ok.stderr
-    assert ok.stdout.strip().splitlines()[-1] == expected
-    # A copy of the pack whose kernel library differs by one appended byte must not import.
-    copy = tmp_path / "lib"
-    shutil.copytree(lib_dir, copy)
-    with (copy / "librk_pa_gfx950.so").open("ab") as stream:
-        stream.write(b"\0")
-    bad = subprocess.run([sys.executable, "-c", _binding_import_script(copy)], capture_output=True, text=True,
-                         timeout=300)
-    assert bad.returncode != 0
-    assert "this module was built against" in bad.stderr
+    alone = tmp_path / binary.stem
+    alone.mkdir()
+    shutil.copy2(binary, alone / binary.name)
+    script = (
+        "import importlib.util, torch\n"
+        f"spec = importlib.util.spec_from_file_location('{binary.stem}', r'{alone / binary.name}')\n"
+        "m = importlib.util.module_from_spec(spec); spec.loader.exec_module(m)\n"
+        f"assert all(callable(getattr(m, name)) for name in {entrypoints!r})\n"
+        "print(m.version())\n"
+    )
+    return subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+
+
+def test_bindings_are_self_contained(tmp_path):
+    """Each binding carries its kernels: it imports with no other file of the pack beside it, so a
+    release archive of the manifest, its signature and the named artifacts is complete."""
+
+    run = _import_alone(tmp_path, PACK / "lib" / "rk_pa_gfx950.so", ("decode_mfma", "decode_valu"))
+    assert run.returncode == 0, run.stderr
+    assert run.stdout.strip().splitlines()[-1] == "rk_pa_gfx950 1.0.0 (gfx950, wave64)"
 
 
 # ---------------------------------------------------------------------------------------------
@@ -247,12 +241,8 @@ def test_kv_entries_merge_into_the_reference_manifest():
         assert decision.entry_id == entry.id
 
 
-def test_pack_lists_every_binding_and_kv_bindings_pin_their_library():
-    import subprocess
-    import sys
-
+def test_pack_lists_every_binding_and_kv_bindings_are_self_contained(tmp_path):
     pack = KernelPack.from_directory(PACK, verify_artifacts=False)
-    expected = hashlib.sha256((PACK / "lib" / "librk_kv_gfx950.so").read_bytes()).hexdigest()
     for operator in ("kv_cache_append", "kv_cache_copy"):
         item = pack.get(operator, "1.0")
         manifest = builtin_dispatch_registry().get(operator, "1.0")
@@ -261,16 +251,9 @@ def test_pack_lists_every_binding_and_kv_bindings_pin_their_library():
         if not binary.is_file():
             pytest.fail("the kernel pack is not built; run __graft_entry__.build()")
         assert hashlib.sha256(binary.read_bytes()).hexdigest() == item.artifact.sha256
-        script = (
-            "import importlib.util, torch\n"
-            f"spec = importlib.util.spec_from_file_location('{binary.name.split('.')[0]}', r'{binary}')\n"
-            "m = importlib.util.module_from_spec(spec); spec.loader.exec_module(m)\n"
-            f"assert callable(m.{item.artifact.entrypoint})\n"
-            "print(m.kernel_library_sha256)\n"
-        )
-        run = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+        run = _import_alone(tmp_path, binary, (item.artifact.entrypoint,))
         assert run.returncode == 0, run.stderr
-        assert run.stdout.strip().splitlines()[-1] == expected
+        assert run.stdout.strip().splitlines()[-1] == "rk_kv_gfx950 1.0.0 (gfx950, wave64)"
 
 
 def copy_signature(case, dtype="bf16", index="int64"):

@@ -20,6 +20,12 @@ from radeon_kernels.providers.native import NativeProviderError
 from radeon_kernels.runtime.explain import clear_last_dispatch, get_last_dispatch
 from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint
 from radeon_kernels.runtime.packs import KernelPackRegistry, PackResolutionError, default_pack_roots
+from radeon_kernels.runtime.ed25519 import Ed25519PrivateKey
+from radeon_kernels.runtime.signing import TrustedKey, TrustedKeyring, signature_document
+
+TEST_KEY = Ed25519PrivateKey.from_private_bytes(hashlib.sha256(b"rk-test-pack-key").digest())
+TEST_KEYRING = TrustedKeyring([TrustedKey("rk-test", TEST_KEY.public_key().public_bytes(), "active",
+                                          "2026-12-01T00:00:00+00:00")])
 from radeon_kernels.runtime.registry import ArtifactSpec, DispatchManifest, DispatchRegistry
 
 ENV = {"architecture": "gfx950", "wavefront_size": 64, "rocm_abi": "7.0", "python_abi": "cp310",
@@ -184,13 +190,20 @@ def write_pack(root: Path, *, env=None, digest=None, evidence="evidence-pa", ext
     if extra:
         document.update(extra)
     (root / "manifest.json").write_text(json.dumps(document), encoding="utf-8")
+    sign_manifest(root)
     return hashlib.sha256(artifact.read_bytes()).hexdigest()
+
+
+def sign_manifest(root: Path, key=TEST_KEY, key_id="rk-test"):
+    digest = hashlib.sha256((root / "manifest.json").read_bytes()).hexdigest()
+    envelope = signature_document(private_key=key, key_id=key_id, signed_file="manifest.json", signed_sha256=digest)
+    (root / "manifest.sig.json").write_text(json.dumps(envelope), encoding="utf-8")
 
 
 def test_pack_discovery_resolution_and_end_to_end(tmp_path):
     digest = write_pack(tmp_path / "packs" / "gfx950")
     write_pack(tmp_path / "packs" / "broken", extra={"unexpected": 1})
-    registry = KernelPackRegistry.discover([tmp_path / "packs"])
+    registry = KernelPackRegistry.discover([tmp_path / "packs"], trusted_keys=TEST_KEYRING)
     assert [p.pack_id for p in registry.packs] == ["rk-pa-test"]
     assert len(registry.rejected) == 1 and "unknown fields" in registry.rejected[0]
     spec = ArtifactSpec("native", "lib/pa.py", "decode_mfma", digest)
@@ -213,7 +226,7 @@ def test_pack_discovery_resolution_and_end_to_end(tmp_path):
 def test_corrupted_artifact_demotes(tmp_path):
     digest = write_pack(tmp_path / "packs" / "gfx950")
     (tmp_path / "packs" / "gfx950" / "lib" / "pa.py").write_text("def decode_mfma(*a, **k):\n    return 'tampered'\n")
-    registry = KernelPackRegistry.discover([tmp_path / "packs"])
+    registry = KernelPackRegistry.discover([tmp_path / "packs"], trusted_keys=TEST_KEYRING)
     clear_last_dispatch()
     runtime = OperatorRuntime(registry=DispatchRegistry([manifest(winner=True, digest=digest)]),
                               pack_registry=registry, fingerprint_detector=lambda **_: fingerprint())
@@ -222,14 +235,40 @@ def test_corrupted_artifact_demotes(tmp_path):
     assert "SHA-256 mismatch" in get_last_dispatch()["reason"]
 
 
-def test_signature_requirement_without_verifier_rejects_packs(tmp_path):
-    write_pack(tmp_path / "packs" / "gfx950")
-    registry = KernelPackRegistry.discover([tmp_path / "packs"], require_signatures=True)
-    assert registry.packs == () and "no signature verifier" in registry.rejected[0]
-    seen = []
-    verified = KernelPackRegistry.discover([tmp_path / "packs"], require_signatures=True,
-                                           signature_verifier=seen.append)
-    assert len(verified.packs) == 1 and seen == [(tmp_path / "packs" / "gfx950").resolve()]
+def test_packs_load_only_with_a_valid_manifest_signature(tmp_path):
+    """The registry verifies manifest.sig.json before reading a pack (reference packs.py:88-113)."""
+
+    root = tmp_path / "packs"
+    write_pack(root / "signed")
+    write_pack(root / "unsigned")
+    (root / "unsigned" / "manifest.sig.json").unlink()
+    write_pack(root / "tampered")
+    manifest = root / "tampered" / "manifest.json"
+    manifest.write_text(manifest.read_text().replace("rk-pa-test", "rk-pa-test-2"))
+    write_pack(root / "other-key")
+    sign_manifest(root / "other-key", key=Ed25519PrivateKey.from_private_bytes(b"\1" * 32))
+    write_pack(root / "unknown-key")
+    sign_manifest(root / "unknown-key", key_id="rk-unknown")
+    registry = KernelPackRegistry.discover([root], trusted_keys=TEST_KEYRING)
+    assert [p.root.name for p in registry.packs] == ["signed"]
+    reasons = {Path(line.split(":", 1)[0]).name: line for line in registry.rejected}
+    assert "cannot read detached signature" in reasons["unsigned"]
+    assert "SHA-256 mismatch" in reasons["tampered"]
+    assert "invalid Ed25519 signature" in reasons["other-key"]
+    assert "unknown key 'rk-unknown'" in reasons["unknown-key"]
+    revoked = TrustedKeyring([TrustedKey("rk-test", TEST_KEY.public_key().public_bytes(), "revoked",
+                                         "2026-12-01T00:00:00+00:00", "test")])
+    assert KernelPackRegistry.discover([root / "signed"], trusted_keys=revoked).packs == ()
+    assert len(KernelPackRegistry.discover([root], require_signatures=False).packs) == 5
+
+
+def test_in_tree_pack_is_signed_by_a_key_of_the_builtin_keyring():
+    from radeon_kernels.runtime.packs import IN_TREE_PACK_ROOT
+
+    if not (IN_TREE_PACK_ROOT / "gfx950" / "manifest.json").is_file():
+        pytest.fail("the kernel pack is not built; run __graft_entry__.build()")
+    registry = KernelPackRegistry.discover([IN_TREE_PACK_ROOT])
+    assert [p.pack_id for p in registry.packs] == ["rk-paged-attention-gfx950"] and registry.rejected == ()
 
 
 def test_default_pack_roots_order(tmp_path):

@@ -28,6 +28,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5] [--va
                        [--cpu-seconds S] [--calibration-copy]
        python bench.py --operator kv_cache_append|kv_cache_copy [--case ...] [--dtype bf16]
                        (the paged-cache operators around the decode; same JSON line shape)
+       python bench.py --operator sdpa [--case ...] [--dtype bf16]
+                       (prefill self-attention; roofline against the dense MFMA peak)
 """
 
 from __future__ import annotations
@@ -67,11 +69,13 @@ def parse_args(argv=None):
     parser.add_argument("--calibration-copy", action="store_true",
                         help="run a 1 GiB device copy before timing (counter calibration under rocprofv3)")
     parser.add_argument("--operator", default="paged_attention_decode",
-                        choices=["paged_attention_decode", "kv_cache_append", "kv_cache_copy"])
+                        choices=["paged_attention_decode", "kv_cache_append", "kv_cache_copy", "sdpa"])
     parser.add_argument("--case", default=None,
-                        help="kv_cache_append / kv_cache_copy case (benchmarks/workloads/kv_cache_*-1.0.yaml in the "
-                             "reference); defaults: prefill-t128-mha32-d128-p32, beam-pairs64-gqa8-d256-p16")
-    parser.add_argument("--dtype", default="bf16", choices=["fp16", "bf16"], help="KV-cache operator element type")
+                        help="kv_cache_append / kv_cache_copy / sdpa case (benchmarks/workloads/<operator>-1.0.yaml "
+                             "in the reference, or an sdpa long-prefill case); defaults: prefill-t128-mha32-d128-p32, "
+                             "beam-pairs64-gqa8-d256-p16, b4-gqa32x8-s4096-d128-causal")
+    parser.add_argument("--dtype", default="bf16", choices=["fp16", "bf16"],
+                        help="element type of the KV-cache and sdpa operators")
     return parser.parse_args(argv)
 
 
@@ -170,6 +174,126 @@ def cpu_baseline(torch, data, seconds: float) -> dict:
                    f"oracle/pa_oracle.py (torch {torch.__version__} CPU, {threads} threads), {elapsed:.1f} s"),
         "us_per_call_extrapolated": round(data["kv_bytes"] / (gbps * 1e9) * 1e6, 1),
     }
+
+
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA
+
+
+def main_sdpa(args) -> int:
+    """``--operator sdpa``: one step = one self-attention forward call of the case (one kernel)."""
+
+    import torch
+
+    from radeon_kernels.cabi import sdpa_library
+    from radeon_kernels.workloads import SDPA_CASES, SDPA_LONG_CASES, make_sdpa_inputs
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no visible ROCm GPU"}))
+        return 1
+    device = torch.device("cuda:0")
+    lib = sdpa_library()  # raises if the HIP library was not built
+    cases = {**SDPA_CASES, **SDPA_LONG_CASES}
+    case = cases[args.case or "b4-gqa32x8-s4096-d128-causal"]
+    data = make_sdpa_inputs(case, dtype=args.dtype, device=device, generator_device=device)
+    q, k, v = data["query"], data["key"], data["value"]
+    scale = 1.0 / math.sqrt(case.head_dim)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream(device)
+
+    def launch():
+        lib.forward(q, k, v, is_causal=case.causal, scale=scale, out=out, stream=stream)
+
+    for _ in range(args.warmup):
+        launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    us_per_call = (time.perf_counter() - t) / args.steps * 1e6
+    kernel_us = start.elapsed_time(end) * 1e3 / args.steps
+    flops = case.flops()
+
+    import warnings
+
+    import radeon_kernels as rk
+    from radeon_kernels.ops._runtime import NativeDemotionWarning
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", NativeDemotionWarning)
+        rk.sdpa(q, k, v, is_causal=case.causal)
+    decision = rk.get_last_dispatch()
+    rk_us = public_call_us(torch, lambda: rk.sdpa(q, k, v, is_causal=case.causal), max(1, args.steps // 5))
+    # The operator's declared fallback on the same GPU (torch's scaled_dot_product_attention).
+    from radeon_kernels.ops.sdpa.reference import sdpa_fallback
+
+    fallback_us = public_call_us(torch, lambda: sdpa_fallback(torch, q, k, v, case.causal, scale),
+                                 max(1, args.steps // 5))
+    result = {
+        "metric": "sdpa prefill TFLOP/s over attended (query, key) pairs (% MI355X dense MFMA peak)",
+        "value": round(flops / (us_per_call * 1e6), 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_per_call / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic (seeded N(0,1) query/key/value)",
+        "config": {
+            "workload": f"sdpa-{case.key}-{args.dtype}", "batch": case.batch, "query_heads": case.query_heads,
+            "kv_heads": case.kv_heads, "sequence": case.sequence, "head_dim": case.head_dim,
+            "causal": case.causal, "reference_case": case.key in SDPA_CASES,
+            "arch": torch.cuda.get_device_properties(0).gcnArchName.split(":", 1)[0],
+        },
+        "us_per_call": round(us_per_call, 2),
+        "flops_per_call": flops,
+        "kernels_us": {"sdpa_fwd_kernel": round(kernel_us, 2)},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(flops / (kernel_us * 1e6), 2),
+            "peak": MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(flops / (kernel_us * 1e6) / MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "rk_call": {"us_per_call": round(rk_us, 2), "selected": decision["selected"], "entry_id": decision["entry_id"]},
+        "torch_sdpa_fallback_us": round(fallback_us, 2),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_sdpa(torch, case, data, min(args.cpu_seconds,
+                                                                                                    10.0)),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline_sdpa(torch, case, data, seconds: float) -> dict:
+    """The reference's explicit fp32 evaluation (restated in oracle/) on the host cores, one
+    (sequence, query head) slice at a time, for about ``seconds``; reported per whole call."""
+
+    from oracle import sdpa_oracle
+
+    q, k, v = (data[n].cpu() for n in ("query", "key", "value"))
+    group = case.query_heads // case.kv_heads
+    scale = 1.0 / math.sqrt(case.head_dim)
+    slices = [(b, h) for b in range(case.batch) for h in range(case.query_heads)]
+    done, t = 0, time.perf_counter()
+    while done < len(slices) and time.perf_counter() - t < seconds:
+        b, h = slices[done]
+        sdpa_oracle.fallback_restated(torch, q[b:b + 1, h:h + 1], k[b:b + 1, h // group:h // group + 1],
+                                      v[b:b + 1, h // group:h // group + 1], case.causal, scale)
+        done += 1
+    elapsed = time.perf_counter() - t
+    per_call = elapsed / done * len(slices)
+    return {"value": round(case.flops() / (per_call * 1e12), 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{done} of {len(slices)} (sequence, query head) slices of the explicit fp32 reference "
+                      f"(oracle/sdpa_oracle.py, torch {torch.__version__} CPU), {elapsed:.1f} s",
+            "us_per_call_extrapolated": round(per_call * 1e6, 1)}
 
 
 def main_kv(args) -> int:
@@ -308,6 +432,8 @@ def cpu_baseline_kv(torch, operator: str, data, moved: int, seconds: float) -> d
 
 def main(argv=None) -> int:
     args = parse_args(argv)
+    if args.gpus == 1 and args.operator == "sdpa":
+        return main_sdpa(args)
     if args.gpus == 1 and args.operator != "paged_attention_decode":
         return main_kv(args)
     if args.gpus != 1:

@@ -7,6 +7,8 @@ Outputs (all under ``radeon-kernels_amd/packs/gfx950``):
 * ``lib/librk_kv_gfx950.so`` -- paged KV-cache C-ABI library (``include/rk_kv_cache.h``).
 * ``lib/rk_kv_append_gfx950.so``, ``lib/rk_kv_copy_gfx950.so`` -- its PyTorch-ROCm bindings, one
   module per operator (a pack names one artifact file per operator), built from one source.
+* ``lib/librk_sdpa_gfx950.so`` -- self-attention (prefill) C-ABI library (``include/rk_sdpa.h``).
+* ``lib/rk_sdpa_gfx950.so`` -- its PyTorch-ROCm binding (module ``rk_sdpa_gfx950``).
 * ``manifest.json``          -- the kernel-pack manifest (same fields as the reference's
   ``schemas/kernel-pack.schema.json``), stamped with the bindings' SHA-256 and this environment.
 
@@ -129,6 +131,7 @@ LIBRARIES = (
     Library("pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", {EXTENSION_NAME: ("paged_attention_decode",)}),
     Library("kv_cache_gfx950.hip", "librk_kv_gfx950.so", "kv_torch_ext.cpp",
             {"rk_kv_append_gfx950": ("kv_cache_append",), "rk_kv_copy_gfx950": ("kv_cache_copy",)}),
+    Library("sdpa_gfx950.hip", "librk_sdpa_gfx950.so", "sdpa_torch_ext.cpp", {"rk_sdpa_gfx950": ("sdpa",)}),
 )
 
 

@@ -266,3 +266,78 @@ def kv_library() -> KvCacheLibrary:
     if _KV_LIBRARY is None:
         _KV_LIBRARY = KvCacheLibrary()
     return _KV_LIBRARY
+
+
+# ---------------------------------------------------------------------------------------------
+# Self-attention library (include/rk_sdpa.h).
+SDPA_LIBRARY_PATH = LIBRARY_PATH.parent / "librk_sdpa_gfx950.so"
+SDPA_EXPORTED_SYMBOLS = ("rk_sdpa_forward", "rk_sdpa_last_error", "rk_sdpa_version")
+RK_SDPA_OK = 0
+RK_SDPA_ERR_INVALID_ARGUMENT = 1
+RK_SDPA_ERR_UNSUPPORTED = 2
+RK_SDPA_ERR_LAUNCH = 4
+
+
+class SdpaLibrary:
+    """ctypes binding of ``librk_sdpa_gfx950.so``; ``forward`` adapts torch tensors to it."""
+
+    def __init__(self, path: Path | str | None = None) -> None:
+        import torch  # noqa: F401  (bind to torch's HIP runtime, see module docstring)
+
+        self.path = Path(path) if path is not None else SDPA_LIBRARY_PATH
+        if not self.path.is_file():
+            raise FileNotFoundError(
+                f"native library {self.path} is missing; build it with `python radeon-kernels_amd/build.py`")
+        lib = ctypes.CDLL(str(self.path))
+        i64, vp = ctypes.c_int64, ctypes.c_void_p
+        lib.rk_sdpa_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_int, ctypes.c_float,
+                                        ctypes.c_int, vp]
+        lib.rk_sdpa_forward.restype = ctypes.c_int
+        lib.rk_sdpa_last_error.argtypes = []
+        lib.rk_sdpa_last_error.restype = ctypes.c_char_p
+        lib.rk_sdpa_version.argtypes = []
+        lib.rk_sdpa_version.restype = ctypes.c_char_p
+        self.lib = lib
+
+    def version(self) -> str:
+        return self.lib.rk_sdpa_version().decode()
+
+    def last_error(self) -> str:
+        return self.lib.rk_sdpa_last_error().decode()
+
+    def forward_raw(self, *, query: int, key: int, value: int, output: int, batch: int, query_heads: int,
+                    kv_heads: int, sequence: int, head_dim: int, is_causal: int, scale: float, dtype: int,
+                    stream: int) -> int:
+        return self.lib.rk_sdpa_forward(query, key, value, output, batch, query_heads, kv_heads, sequence, head_dim,
+                                        is_causal, ctypes.c_float(scale), dtype, stream or None)
+
+    def forward(self, query: Any, key: Any, value: Any, *, is_causal: bool = False, scale: float | None = None,
+                out: Any | None = None, stream: Any | None = None) -> Any:
+        import torch
+
+        batch, query_heads, sequence, head_dim = (int(s) for s in query.shape)
+        if scale is None:
+            scale = 1.0 / math.sqrt(head_dim)
+        if out is None:
+            out = torch.empty_like(query)
+        if stream is None:
+            stream = torch.cuda.current_stream(query.device)
+        status = self.forward_raw(query=query.data_ptr(), key=key.data_ptr(), value=value.data_ptr(),
+                                  output=out.data_ptr(), batch=batch, query_heads=query_heads,
+                                  kv_heads=int(key.shape[1]), sequence=sequence, head_dim=head_dim,
+                                  is_causal=int(bool(is_causal)), scale=float(scale),
+                                  dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
+                                  stream=stream.cuda_stream)
+        if status != RK_SDPA_OK:
+            raise CabiError(status, self.last_error())
+        return out
+
+
+_SDPA_LIBRARY: SdpaLibrary | None = None
+
+
+def sdpa_library() -> SdpaLibrary:
+    global _SDPA_LIBRARY
+    if _SDPA_LIBRARY is None:
+        _SDPA_LIBRARY = SdpaLibrary()
+    return _SDPA_LIBRARY

@@ -16,7 +16,9 @@ Operators and regions:
   4096 workgroups);
 * ``kv_cache_append`` and ``kv_cache_copy``: one exact entry per case of the reference's workload files
   (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18, kv_cache_copy-1.0.yaml:12-17) and one broad
-  gfx950 region each; their bindings (entrypoints ``append`` and ``copy``) share one kernel library.
+  gfx950 region each; their bindings (entrypoints ``append`` and ``copy``) share one kernel source;
+* ``sdpa``: one exact entry per case of benchmarks/workloads/sdpa-1.0.yaml:13-21 (both dtypes) and
+  one broad gfx950 region (the reference publishes no sdpa winner at all: dispatch/sdpa-1.0.json).
 
 Shapes a kernel rejects at launch time (a ValueError) are demoted to the torch fallback by the
 runtime with the reason recorded.  Each operator has its own binding artifact and evidence id; both
@@ -43,6 +45,10 @@ KV_COPY = "kv_cache_copy"
 KV_COPY_EVIDENCE_ID = "mi355x-gfx950-kv_cache_copy-blockcopy-1"
 KV_COPY_ENTRYPOINT = "copy"
 KV_COPY_ARTIFACT = "lib/rk_kv_copy_gfx950.so"
+SDPA = "sdpa"
+SDPA_EVIDENCE_ID = "mi355x-gfx950-sdpa-flash-1"
+SDPA_ENTRYPOINT = "forward"
+SDPA_ARTIFACT = "lib/rk_sdpa_gfx950.so"
 
 _INT_MAX = 2**31 - 1
 _POW2_BLOCKS = [1, 2, 4, 8, 16, 32, 64, 128, 256]
@@ -144,6 +150,39 @@ KV_COPY_BROAD_REGION: dict[str, Any] = {
 }
 
 
+# sdpa: (id suffix, workload constraints).  The reference's cases (benchmarks/workloads/sdpa-1.0.yaml:13-21),
+# each for both dtypes.
+SDPA_EXACT_REGIONS: list[tuple[str, dict[str, Any]]] = [
+    (case, {"batch": b, "query_heads": hq, "kv_heads": hkv, "sequence": s, "head_dim": d,
+            "attention_mode": "causal" if causal else "noncausal"})
+    for case, b, hq, hkv, s, d, causal in (
+        ("b1-mha16-s128-d64-causal", 1, 16, 16, 128, 64, True),
+        ("b1-gqa32x8-s128-d128-causal", 1, 32, 8, 128, 128, True),
+        ("b1-gqa32x8-s256-d128-causal", 1, 32, 8, 256, 128, True),
+        ("b1-gqa32x8-s512-d128-causal", 1, 32, 8, 512, 128, True),
+        ("b4-gqa32x8-s128-d128-causal", 4, 32, 8, 128, 128, True),
+        ("b8-gqa32x8-s64-d128-causal", 8, 32, 8, 64, 128, True),
+        ("b1-mha16-s256-d64-noncausal", 1, 16, 16, 256, 64, False),
+        ("b2-gqa16x4-s256-d256-causal", 2, 16, 4, 256, 256, True),
+    )
+]
+SDPA_BROAD_REGION: dict[str, Any] = {
+    "batch": [1, 65535],
+    "query_heads": [1, 65535],
+    "kv_heads": [1, 65535],
+    "sequence": [1, (1 << 30) - 1],
+    "head_dim": {"one_of": [64, 128, 256]},
+    "attention_mode": {"one_of": ["causal", "noncausal"]},
+}
+_SDPA_COMMON = {
+    "dtype": {"one_of": ["fp16", "bf16"]},
+    "layout": "batch_head_sequence_dim",
+    "scale_mode": {"one_of": ["default", "explicit"]},
+    "contiguous": True,
+    "requires_grad": False,
+}
+
+
 def _winner(artifact: str, entrypoint: str, sha256: str) -> dict[str, Any]:
     return {"provider": "native", "artifact": artifact, "entrypoint": entrypoint, "sha256": sha256,
             "format": "python_extension"}
@@ -184,6 +223,12 @@ def render_dispatch_manifest(operator: str, *, environment: dict[str, Any], sha2
                           KV_COPY_EVIDENCE_ID) for suffix, region in KV_COPY_EXACT_REGIONS]
         entries.append(_entry(KV_COPY, "region", 10, environment, {**KV_COPY_BROAD_REGION, **_KV_COMMON}, winner,
                               {}, KV_COPY_EVIDENCE_ID))
+    elif operator == SDPA:
+        winner = _winner(SDPA_ARTIFACT, SDPA_ENTRYPOINT, sha256)
+        entries = [_entry(SDPA, suffix, 100, environment, {**region, **_SDPA_COMMON}, winner, {}, SDPA_EVIDENCE_ID)
+                   for suffix, region in SDPA_EXACT_REGIONS]
+        entries.append(_entry(SDPA, "region", 10, environment, {**SDPA_BROAD_REGION, **_SDPA_COMMON}, winner, {},
+                              SDPA_EVIDENCE_ID))
     else:
         raise KeyError(operator)
     return {
@@ -205,6 +250,8 @@ def render_pack_manifest(*, environment: dict[str, Any], digests: dict[str, str]
          **_winner(KV_ARTIFACT, KV_ENTRYPOINT, digests[KV_APPEND]), "evidence_id": KV_EVIDENCE_ID},
         {"operator": KV_COPY, "semantic_version": SEMANTIC_VERSION,
          **_winner(KV_COPY_ARTIFACT, KV_COPY_ENTRYPOINT, digests[KV_COPY]), "evidence_id": KV_COPY_EVIDENCE_ID},
+        {"operator": SDPA, "semantic_version": SEMANTIC_VERSION,
+         **_winner(SDPA_ARTIFACT, SDPA_ENTRYPOINT, digests[SDPA]), "evidence_id": SDPA_EVIDENCE_ID},
     ]
     return {
         "schema_version": "1.0",

@@ -284,3 +284,56 @@ def make_copy_inputs(case: CopyCase | str, *, dtype: str = "bf16", index_dtype: 
     mapping = mapping.to(torch.int64 if index_dtype == "int64" else torch.int32).contiguous()
     out = {"key_cache": key_cache, "value_cache": value_cache, "block_mapping": mapping}
     return {name: tensor.to(device) for name, tensor in out.items()} | {"case": case, "seed": seed}
+
+
+# ---------------------------------------------------------------------------------------------
+# sdpa (prefill self-attention): the reference's cases (benchmarks/workloads/sdpa-1.0.yaml:13-21) and
+# two long-prefill shapes of this build that fill the chip (not reference workloads).
+@dataclass(frozen=True)
+class SdpaCase:
+    key: str
+    batch: int
+    query_heads: int
+    kv_heads: int
+    sequence: int
+    head_dim: int
+    causal: bool
+
+    def flops(self) -> int:
+        """Algorithmic FLOPs: 2 (QK^T) + 2 (PV) per head dim per attended (query, key) pair."""
+
+        pairs = self.sequence * (self.sequence + 1) // 2 if self.causal else self.sequence * self.sequence
+        return 4 * self.batch * self.query_heads * self.head_dim * pairs
+
+
+SDPA_CASES = {case.key: case for case in (
+    SdpaCase("b1-mha16-s128-d64-causal", 1, 16, 16, 128, 64, True),
+    SdpaCase("b1-gqa32x8-s128-d128-causal", 1, 32, 8, 128, 128, True),
+    SdpaCase("b1-gqa32x8-s256-d128-causal", 1, 32, 8, 256, 128, True),
+    SdpaCase("b1-gqa32x8-s512-d128-causal", 1, 32, 8, 512, 128, True),
+    SdpaCase("b4-gqa32x8-s128-d128-causal", 4, 32, 8, 128, 128, True),
+    SdpaCase("b8-gqa32x8-s64-d128-causal", 8, 32, 8, 64, 128, True),
+    SdpaCase("b1-mha16-s256-d64-noncausal", 1, 16, 16, 256, 64, False),
+    SdpaCase("b2-gqa16x4-s256-d256-causal", 2, 16, 4, 256, 256, True),
+)}
+SDPA_LONG_CASES = {case.key: case for case in (
+    SdpaCase("b4-gqa32x8-s4096-d128-causal", 4, 32, 8, 4096, 128, True),
+    SdpaCase("b4-gqa32x8-s4096-d128-noncausal", 4, 32, 8, 4096, 128, False),
+)}
+SDPA_SEED = 20261501
+
+
+def make_sdpa_inputs(case: SdpaCase | str, *, dtype: str = "bf16", seed: int = SDPA_SEED, device: Any = "cpu",
+                     generator_device: Any = "cpu") -> dict[str, Any]:
+    """Seeded N(0, 1) query/key/value of one case (generated on ``generator_device``)."""
+
+    import torch
+
+    c = case if isinstance(case, SdpaCase) else {**SDPA_CASES, **SDPA_LONG_CASES}[case]
+    gen = torch.Generator(device=generator_device).manual_seed(seed)
+    dt = torch_dtype(torch, dtype)
+    shape_q = (c.batch, c.query_heads, c.sequence, c.head_dim)
+    shape_kv = (c.batch, c.kv_heads, c.sequence, c.head_dim)
+    tensors = {name: torch.randn(shape, generator=gen, device=generator_device).to(dt).to(device)
+               for name, shape in (("query", shape_q), ("key", shape_kv), ("value", shape_kv))}
+    return {**tensors, "case": c}

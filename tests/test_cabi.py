@@ -276,3 +276,47 @@ def test_kv_copy_invalid_arguments_are_rejected_before_launch(kvlib, overrides, 
     got, text = kv_copy_call(kvlib, **overrides)
     assert got == status, text
     assert message in text
+
+
+# ---------------------------------------------------------------------------------------------
+# Self-attention library (include/rk_sdpa.h).
+SDPA_HEADER = ROOT / "include" / "rk_sdpa.h"
+
+
+@pytest.fixture(scope="module")
+def sdpalib():
+    if not cabi.SDPA_LIBRARY_PATH.is_file():
+        pytest.fail(f"{cabi.SDPA_LIBRARY_PATH} is not built; run __graft_entry__.build()")
+    return cabi.SdpaLibrary()
+
+
+def test_sdpa_header_and_library_agree(sdpalib):
+    text = SDPA_HEADER.read_text()
+    declared = sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(rk_\w+)\s*\(", text, flags=re.MULTILINE)))
+    assert declared == sorted(cabi.SDPA_EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(sdpalib.lib, name), name
+    for name in ("RK_SDPA_OK", "RK_SDPA_ERR_INVALID_ARGUMENT", "RK_SDPA_ERR_UNSUPPORTED", "RK_SDPA_ERR_LAUNCH"):
+        assert getattr(cabi, name) == int(re.search(rf"#define {name} (\d+)", text).group(1)), name
+    assert int(re.search(r"#define RK_SDPA_DTYPE_BF16 (\d+)", text).group(1)) == cabi.RK_DTYPE_BF16
+    assert sdpalib.version() == "rk_sdpa_gfx950 1.0.0 (gfx950, wave64)"
+
+
+@cpu_only
+@pytest.mark.parametrize("overrides, status, message", [
+    (dict(query=0), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "must not be NULL"),
+    (dict(dtype=3), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "dtype"),
+    (dict(sequence=0), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "positive"),
+    (dict(head_dim=96), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "one of 64, 128, 256"),
+    (dict(query_heads=12, kv_heads=8), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "divisible"),
+    (dict(is_causal=2), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "is_causal"),
+    (dict(scale=float("nan")), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "positive and finite"),
+    (dict(output=104), cabi.RK_SDPA_ERR_UNSUPPORTED, "16-byte aligned"),
+    (dict(batch=1024, query_heads=64, kv_heads=8), cabi.RK_SDPA_ERR_UNSUPPORTED, "launch limits"),
+])
+def test_sdpa_invalid_arguments_are_rejected_before_launch(sdpalib, overrides, status, message):
+    args = dict(query=16, key=32, value=48, output=96, batch=1, query_heads=8, kv_heads=2, sequence=64,
+                head_dim=128, is_causal=1, scale=0.125, dtype=cabi.RK_DTYPE_BF16, stream=0)
+    args.update(overrides)
+    assert sdpalib.forward_raw(**args) == status
+    assert message in sdpalib.last_error()

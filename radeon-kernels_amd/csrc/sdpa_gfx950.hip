@@ -18,10 +18,17 @@
 //                    dtype, are already laid out as the B operand of O^T += V^T P^T, whose A operand
 //                    comes from ds_read_b64_tr_b16 transposing reads of the row-major V tile (the
 //                    keys of one MFMA k-step are taken in the order the S^T accumulator holds them,
-//                    which the transposing read reproduces by the addresses it is given).  The next
-//                    block's K and V rows are loaded into registers while the current block is used.
-//                    With the causal mask, blocks past a wave's last query are skipped and query
-//                    blocks are scheduled longest first.
+//                    which the transposing read reproduces by the addresses it is given).  The
+//                    accumulator is rescaled only when some lane's running maximum moved.  The
+//                    register budget is held to three workgroups per CU (at most 170 VGPRs), so one
+//                    workgroup's softmax and LDS traffic overlap another's MFMAs; K and V rows go
+//                    global -> registers -> LDS at the top of each block rather than being
+//                    prefetched a block ahead, which would cost the registers of the third
+//                    workgroup (measured: 1.3x slower on the long causal case).  With the causal
+//                    mask, blocks past a wave's last query are skipped and the grid runs the longest
+//                    query blocks of every head first (1.7x over head-major order on the long
+//                    causal case); without it, neighbouring query blocks of one head run together
+//                    and share its K and V rows in L2.
 //
 // Scores are kept in the base-2 domain: x = (q . k) * scale * log2(e), p = exp2(x - m).
 #include <hip/hip_runtime.h>
@@ -100,7 +107,7 @@ struct Params {
 };
 
 template <class E, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
   constexpr int KS = D / 16;                      // MFMA k-steps of S^T (16 dims each)
   constexpr int DT = D / 32;                      // 32-dim tiles of O^T
@@ -117,9 +124,10 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(Params p) {
   const int half = lane >> 5;
   const int col = lane & 31;
 
-  // Longest query blocks first under the causal mask (their key range is the longest).
-  const int qb = CAUSAL ? p.q_blocks - 1 - static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x);
-  const int bh = blockIdx.y;  // b * Hq + hq
+  // Causal: x = (sequence, head), y = query block, longest first (the key range grows with the
+  // query block).  Otherwise x = query block, y = (sequence, head).
+  const int bh = CAUSAL ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.y);  // b * Hq + hq
+  const int qb = CAUSAL ? p.q_blocks - 1 - static_cast<int>(blockIdx.y) : static_cast<int>(blockIdx.x);
   const int b = bh / p.query_heads;
   const int hq = bh - b * p.query_heads;
   const int hkv = hq / p.group;
@@ -142,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(Params p) {
   const int kv_end = CAUSAL ? min(S, (qb + 1) * kBlockM) : S;
   const int n_blocks = (kv_end + kBlockN - 1) / kBlockN;
 
-  // Register staging of one K and one V block: chunk c of this thread is row (tid + c*256) / ROW_CHUNKS.
+  // Staging of one K and one V block through registers: chunk c of this thread is row (tid + c*256) / ROW_CHUNKS.
   u32x4 kreg[LOADS], vreg[LOADS];
   auto load_block = [&](int kb) {
 #pragma unroll
@@ -179,12 +187,11 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(Params p) {
   const int tr_row = 4 * (g >> 1) + (j16 >> 2);
   const int tr_col = 16 * (g & 1) + 4 * (j16 & 3);
 
-  load_block(0);
   for (int nb = 0; nb < n_blocks; ++nb) {
+    load_block(nb);
     __syncthreads();  // every wave is done with the previous block's LDS tiles
     store_block();
     __syncthreads();
-    if (nb + 1 < n_blocks) load_block(nb + 1);  // in flight while this block is used
 
     const int kb0 = nb * kBlockN;
     if (CAUSAL && kb0 > q_wave + 31) continue;  // no key of this block is visible to this wave
@@ -231,11 +238,13 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(Params p) {
         pb[t][r >> 1] = E::pack(p0, p1);
       }
     l_half = l_half * alpha + psum;
+    if (__builtin_amdgcn_ballot_w64(m_new != m)) {  // alpha == 1 in every lane leaves acc unchanged
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+    }
     m = m_new;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
 
     // O^T += V^T P^T over four k-steps of 16 keys (k-step st covers keys 16 st .. 16 st + 15).
 #pragma unroll
@@ -327,7 +336,7 @@ extern "C" int rk_sdpa_forward(const void* query, const void* key, const void* v
   if (!aligned16(query) || !aligned16(key) || !aligned16(value) || !aligned16(output))
     return fail(RK_SDPA_ERR_UNSUPPORTED, "query, key, value and output must be 16-byte aligned");
   const int64_t q_blocks = (sequence + kBlockM - 1) / kBlockM;
-  if (batch * query_heads >= 65536 || q_blocks >= (int64_t{1} << 31) ||
+  if (batch * query_heads >= 65536 || q_blocks >= 65536 ||
       batch * query_heads * sequence * head_dim >= (int64_t{1} << 62) || sequence >= (int64_t{1} << 30))
     return fail(RK_SDPA_ERR_UNSUPPORTED, "shape exceeds the launch limits of this kernel");
 
@@ -343,7 +352,8 @@ extern "C" int rk_sdpa_forward(const void* query, const void* key, const void* v
   prm.seq = static_cast<int32_t>(sequence);
   prm.q_blocks = static_cast<int32_t>(q_blocks);
   prm.scale_log2e = scale * kLog2e;
-  const dim3 grid(static_cast<uint32_t>(q_blocks), static_cast<uint32_t>(batch * query_heads));
+  const dim3 grid = is_causal ? dim3(static_cast<uint32_t>(batch * query_heads), static_cast<uint32_t>(q_blocks))
+                              : dim3(static_cast<uint32_t>(q_blocks), static_cast<uint32_t>(batch * query_heads));
   hipStream_t hs = static_cast<hipStream_t>(stream);
   if (dtype == RK_SDPA_DTYPE_BF16)
     launch_e<Bf16>(prm, head_dim, is_causal != 0, grid, hs);

@@ -44,13 +44,16 @@ SEEDS_PER_CASE = 3
 WARMUPS = 20  # calls of each side before calibration (benchmarks/workloads/*-1.0.yaml: warmups 20, samples 30)
 # Oracle and baseline names of benchmarks/workloads/<operator>-1.0.yaml:4-5.
 METHODS = {"paged_attention_decode": "torch_fp32_paged_reference", "kv_cache_append": "torch_index_copy",
-           "kv_cache_copy": "torch_snapshot_index_copy"}
+           "kv_cache_copy": "torch_snapshot_index_copy", "sdpa": "torch_fp32_explicit_attention"}
+SDPA_BASELINE = "torch_scaled_dot_product_attention"  # benchmarks/workloads/sdpa-1.0.yaml:5
+SDPA_TOLERANCE = 0.03  # absolute and relative, contracts/sdpa-1.0.json:23
 
 # Headline workload per operator (the largest one: the timing the evidence reports).
 HEADLINE = {
     "paged_attention_decode": "b128-gqa32x8-ragged-d128-p16-bf16",
     "kv_cache_append": "prefill-t128-mha32-d128-p32",
     "kv_cache_copy": "beam-pairs32-mha32-d128-p32",
+    "sdpa": "b1-gqa32x8-s512-d128-causal",
 }
 # Exact paged-attention dispatch regions -> workload keys of radeon_kernels.workloads.
 PA_WORKLOADS = {
@@ -83,9 +86,10 @@ def candidate_record(operator: str) -> dict:
     from radeon_kernels import dispatch_plan
 
     artifact = {"paged_attention_decode": dispatch_plan.ARTIFACT, "kv_cache_append": dispatch_plan.KV_ARTIFACT,
-                "kv_cache_copy": dispatch_plan.KV_COPY_ARTIFACT}[operator]
-    library = "librk_pa_gfx950.so" if operator == "paged_attention_decode" else "librk_kv_gfx950.so"
-    source = "pa_decode_gfx950.hip" if operator == "paged_attention_decode" else "kv_cache_gfx950.hip"
+                "kv_cache_copy": dispatch_plan.KV_COPY_ARTIFACT, "sdpa": dispatch_plan.SDPA_ARTIFACT}[operator]
+    library, source = {"paged_attention_decode": ("librk_pa_gfx950.so", "pa_decode_gfx950.hip"),
+                       "sdpa": ("librk_sdpa_gfx950.so", "sdpa_gfx950.hip")}.get(
+        operator, ("librk_kv_gfx950.so", "kv_cache_gfx950.hip"))
     pack = PACKAGE_ROOT / "packs" / "gfx950"
     return {"artifact": artifact, "artifact_sha256": sha256_file(pack / artifact),
             "library_sha256": sha256_file(pack / "lib" / library),
@@ -202,6 +206,47 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
             "baseline": f"{METHODS['paged_attention_decode']} ({chunk}-sequence chunks)"}
 
 
+def evaluate_sdpa(torch, samples: int) -> dict:
+    import radeon_kernels as rk
+    from radeon_kernels.ops.sdpa.reference import sdpa_fallback, sdpa_reference
+    from radeon_kernels.workloads import SDPA_CASES, SDPA_SEED, make_sdpa_inputs
+
+    device = torch.device("cuda:0")
+    cases = []
+    for name, case in SDPA_CASES.items():
+        scale = 1.0 / math.sqrt(case.head_dim)
+        for dtype in ("fp16", "bf16"):
+            for seed in range(SDPA_SEED, SDPA_SEED + SEEDS_PER_CASE):
+                data = make_sdpa_inputs(case, dtype=dtype, seed=seed, device=device)
+                q, k, v = data["query"], data["key"], data["value"]
+                sys.stderr.write(f"[case] sdpa {name} {dtype} seed {seed}\n")
+                sys.stderr.flush()
+                out = rk.sdpa(q, k, v, is_causal=case.causal)
+                record = rk.get_last_dispatch()
+                expected = sdpa_reference(torch, q.float(), k.float(), v.float(), case.causal, scale)
+                error = (out.float() - expected).abs()
+                within = bool((error <= SDPA_TOLERANCE + SDPA_TOLERANCE * expected.abs()).all().item())
+                finite = bool(torch.isfinite(out).all().item())
+                runtime_ok = record["selected"] == "native/forward"
+                cases.append({"case_id": f"{name}-{dtype}-seed{seed}", "workload": name, "seed": seed, "dtype": dtype,
+                              "runtime_ok": runtime_ok, "finite": finite,
+                              "max_absolute_error": float(error.max().item()), "tolerance": SDPA_TOLERANCE,
+                              "entry_id": record["entry_id"], "passed": runtime_ok and finite and within})
+    case = SDPA_CASES[HEADLINE["sdpa"]]
+    data = make_sdpa_inputs(case, dtype="bf16", device=device)
+    q, k, v = data["query"], data["key"], data["value"]
+    scale = 1.0 / math.sqrt(case.head_dim)
+    rk.sdpa(q, k, v, is_causal=case.causal)
+    record = rk.get_last_dispatch()
+    entrypoint = winner_entrypoint(record)
+    sys.stderr.write("[case] sdpa headline timing\n")
+    sys.stderr.flush()
+    timing = time_pair(torch, lambda: entrypoint(q, k, v, case.causal, scale),
+                       lambda: sdpa_fallback(torch, q, k, v, case.causal, scale), samples=samples)
+    return {"cases": cases, "timing": timing, "headline_entry_id": record["entry_id"], "oracle": METHODS["sdpa"],
+            "baseline": SDPA_BASELINE}
+
+
 def evaluate_kv(torch, operator: str, samples: int) -> dict:
     import radeon_kernels as rk
     from radeon_kernels.ops.kv_cache.reference import kv_cache_append_reference, kv_cache_copy_reference
@@ -263,7 +308,7 @@ def evaluate_kv(torch, operator: str, samples: int) -> dict:
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--output", type=Path, required=True)
-    parser.add_argument("--operators", default="paged_attention_decode,kv_cache_append,kv_cache_copy")
+    parser.add_argument("--operators", default="paged_attention_decode,kv_cache_append,kv_cache_copy,sdpa")
     parser.add_argument("--samples", type=int, default=30)
     args = parser.parse_args(argv)
 
@@ -278,6 +323,8 @@ def main(argv=None) -> int:
         started = time.perf_counter()
         if operator == "paged_attention_decode":
             result = evaluate_paged_attention(torch, args.samples)
+        elif operator == "sdpa":
+            result = evaluate_sdpa(torch, args.samples)
         else:
             result = evaluate_kv(torch, operator, args.samples)
         document = {"schema": "rk-gfx950-evaluation-1", "operator": operator, "semantic_version": "1.0",

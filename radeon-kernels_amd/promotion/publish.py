@@ -70,7 +70,7 @@ PACK_DIR = PACKAGE_ROOT / "packs" / "gfx950"
 EVALUATIONS = PACKAGE_ROOT / "evaluations"
 RECORD_DIRS = {name: PACKAGE_ROOT / name for name in ("proposals", "approvals", "evidence", "pack-index")}
 RELEASES = PACKAGE_ROOT / "releases"
-OPERATORS = ("paged_attention_decode", "kv_cache_append", "kv_cache_copy")
+OPERATORS = ("paged_attention_decode", "kv_cache_append", "kv_cache_copy", "sdpa")
 MINIMUM_IMPROVEMENT_PCT = 3.0
 MAXIMUM_CV = 0.03
 REVIEWER = "rk-gfx950-build-gates"

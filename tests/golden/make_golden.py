@@ -11,7 +11,7 @@ Writes:
                    boundaries 1, block_size, block_size+1.
   c1_expected.npz  the 1-sequence 32/8-head d128 fp16 workload: SHA-256 of each seeded input
                    tensor, float64 brute-force output and its fp16 rounding.
-  reference_dispatch_{paged_attention_decode,kv_cache_append,kv_cache_copy}-1.0.json
+  reference_dispatch_{paged_attention_decode,kv_cache_append,kv_cache_copy,sdpa}-1.0.json
                    the reference's published dispatch manifests for these operators (data,
                    Apache-2.0), used to prove the gfx950 entries merge into them; copied from
                    /root/reference when that tree is present.
@@ -113,7 +113,7 @@ def main() -> None:
         expected_fp16=pa_oracle.round_to_fp16(expected.astype(np.float32)),
     )
 
-    for operator in ("paged_attention_decode", "kv_cache_append", "kv_cache_copy"):
+    for operator in ("paged_attention_decode", "kv_cache_append", "kv_cache_copy", "sdpa"):
         source = Path(f"/root/reference/dispatch/{operator}-1.0.json")
         if source.is_file():
             document = json.loads(source.read_text(encoding="utf-8"))

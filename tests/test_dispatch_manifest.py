@@ -285,3 +285,37 @@ def test_kv_copy_entries_merge_into_the_reference_manifest():
     merged["entries"].extend(ours["entries"])
     parsed = DispatchManifest.from_mapping(merged, "merged")
     assert len(parsed.entries) == len(reference["entries"]) + len(ours["entries"])
+
+
+# ---------------------------------------------------------------------------------------------
+# sdpa
+def test_sdpa_entries_merge_into_the_reference_fallback_only_manifest():
+    """The reference publishes no sdpa winner (dispatch/sdpa-1.0.json: entries []); appending the gfx950
+    entries gives a valid manifest whose published behaviour elsewhere is unchanged (fallback)."""
+
+    reference = json.loads((GOLDEN / "reference_dispatch_sdpa-1.0.json").read_text())
+    assert reference["entries"] == [] and reference["default_fallbacks"] == ["torch"]
+    ours = json.loads((ROOT / "radeon-kernels_amd" / "radeon_kernels" / "dispatch" / "sdpa-1.0.json").read_text())
+    merged = dict(reference, entries=reference["entries"] + ours["entries"])
+    manifest = DispatchManifest.from_mapping(merged, "merged sdpa")
+    assert len(manifest.entries) == len(dispatch_plan.SDPA_EXACT_REGIONS) + 1
+
+
+@pytest.mark.parametrize("suffix, region", dispatch_plan.SDPA_EXACT_REGIONS)
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_sdpa_reference_cases_select_their_exact_entry(suffix, region, dtype):
+    from radeon_kernels.ops.sdpa.api import _execute as execute_sdpa
+
+    torch_dtype = {"fp16": "float16", "bf16": "bfloat16"}[dtype]
+    q = FakeTensor((region["batch"], region["query_heads"], region["sequence"], region["head_dim"]), dtype=torch_dtype)
+    kv = FakeTensor((region["batch"], region["kv_heads"], region["sequence"], region["head_dim"]), dtype=torch_dtype)
+    runtime = CaptureRuntime()
+    execute_sdpa(q, kv, kv, region["attention_mode"] == "causal", torch_module=FakeTorch(), runtime=runtime)
+    signature = runtime.call["signature"]
+    decision = Dispatcher(builtin_dispatch_registry()).select(DispatchRequest("sdpa", "1.0", signature),
+                                                              gfx950_fingerprint())
+    assert decision.entry_id == f"sdpa-gfx950-{suffix}" and decision.launch == {}
+    other = dict(signature, sequence=region["sequence"] + 1)
+    decision = Dispatcher(builtin_dispatch_registry()).select(DispatchRequest("sdpa", "1.0", other),
+                                                              gfx950_fingerprint())
+    assert decision.entry_id == "sdpa-gfx950-region"

@@ -30,7 +30,9 @@
 //                    causal case); without it, neighbouring query blocks of one head run together
 //                    and share its K and V rows in L2.
 //
-// Scores are kept in the base-2 domain: x = (q . k) * scale * log2(e), p = exp2(x - m).
+// Scores are kept in the base-2 domain: p = exp2((q . k) * scale * log2(e) - m), evaluated as one
+// fused multiply-add per score; the running maximum m is taken on the raw dot products (scale > 0
+// keeps their order) and scaled once per block.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -218,13 +220,13 @@ __global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kb0 + 32 * t + 8 * (r >> 2) + 4 * half + (r & 3);
-        float value = s[t][r] * p.scale_log2e;
+        float value = s[t][r];
         if (masked && (key >= S || (CAUSAL && key > my_q))) value = neg_inf;
         x[t][r] = value;
         mx = fmaxf(mx, value);
       }
     mx = max_halves(mx);
-    const float m_new = fmaxf(m, mx);
+    const float m_new = fmaxf(m, mx * p.scale_log2e);
     const float m_use = m_new == neg_inf ? 0.f : m_new;  // a query with no visible key yet
     const float alpha = fast_exp2(m - m_use);            // 0 while m = -inf
     float psum = 0.f;
@@ -233,7 +235,8 @@ __global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float p0 = fast_exp2(x[t][r] - m_use), p1 = fast_exp2(x[t][r + 1] - m_use);
+        const float p0 = fast_exp2(fmaf(x[t][r], p.scale_log2e, -m_use));
+        const float p1 = fast_exp2(fmaf(x[t][r + 1], p.scale_log2e, -m_use));
         psum += p0 + p1;
         pb[t][r >> 1] = E::pack(p0, p1);
       }

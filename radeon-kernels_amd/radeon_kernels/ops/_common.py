@@ -80,3 +80,24 @@ def tensor_context(torch_module: Any, operator: str, *tensors: Any) -> TensorCon
         contiguous=all(bool(item.is_contiguous()) for item in tensors),
         requires_grad=any(bool(item.requires_grad) for item in tensors),
     )
+
+
+def call_key(torch_module: Any, operator: str, tensors: tuple[Any, ...], extra: Any = None) -> tuple | None:
+    """Exact, hashable description of everything validation reads from a call, or None.
+
+    Per tensor: its type (the ``isinstance`` check), dtype, device, ``is_cuda``, shape (which fixes
+    ``dim()``), contiguity and ``requires_grad``; plus the operator, the torch module the dtypes are
+    compared with, and ``extra`` (the call's non-tensor arguments).  Two calls with equal keys pass
+    or fail every check identically and build the same dispatch signature, which is what lets the
+    operator runtime reuse a call plan.  Anything unusual about the inputs (a missing attribute, a
+    raising property) gives None, and the call then takes the fully validated path.
+    """
+
+    try:
+        key = [operator, torch_module, extra]
+        for tensor in tensors:
+            key += (type(tensor), tensor.dtype, tensor.device, tensor.is_cuda, tensor.shape,
+                    tensor.is_contiguous(), tensor.requires_grad)
+        return tuple(key)
+    except Exception:
+        return None

@@ -13,6 +13,7 @@ from __future__ import annotations
 from typing import Any
 
 from radeon_kernels.ops._common import (
+    call_key,
     index_dtype_name,
     tensor_context,
     torch_runtime,
@@ -68,6 +69,7 @@ def _execute_append(
     *,
     torch_module: Any,
     runtime: OperatorRuntime,
+    plan_key: Any = None,
 ) -> tuple[Any, Any]:
     op = APPEND
     validate_tensor(torch_module, key, name="key", rank=3, operator=op)
@@ -111,8 +113,26 @@ def _execute_append(
         native_arguments=(key, value, key_cache, value_cache, slot_mapping),
         fallback=lambda: kv_cache_append_reference(torch_module, key, value, key_cache, value_cache, slot_mapping),
         fallback_selected=FALLBACK_SELECTED,
+        plan_key=plan_key,
     )
     return _returned_caches(op, result, key_cache, value_cache)
+
+
+def _dispatch_append(key: Any, value: Any, key_cache: Any, value_cache: Any, slot_mapping: Any, *,
+                     torch_module: Any, runtime: OperatorRuntime) -> tuple[Any, Any]:
+    """A call shape validated before runs its kept plan; any other call takes ``_execute_append``."""
+
+    plan_key = call_key(torch_module, APPEND, (key, value, key_cache, value_cache, slot_mapping))
+    plan = runtime.plan_for(plan_key)
+    if plan is None:
+        return _execute_append(key, value, key_cache, value_cache, slot_mapping, torch_module=torch_module,
+                               runtime=runtime, plan_key=plan_key)
+    result = runtime.run_plan(
+        plan, (key, value, key_cache, value_cache, slot_mapping),
+        lambda: kv_cache_append_reference(torch_module, key, value, key_cache, value_cache, slot_mapping),
+        FALLBACK_SELECTED,
+    )
+    return _returned_caches(APPEND, result, key_cache, value_cache)
 
 
 def kv_cache_append(key: Any, value: Any, key_cache: Any, value_cache: Any, slot_mapping: Any) -> tuple[Any, Any]:
@@ -123,8 +143,8 @@ def kv_cache_append(key: Any, value: Any, key_cache: Any, value_cache: Any, slot
     unique).  Updates the caches in place and returns them.
     """
 
-    return _execute_append(key, value, key_cache, value_cache, slot_mapping, torch_module=_torch(),
-                           runtime=default_operator_runtime())
+    return _dispatch_append(key, value, key_cache, value_cache, slot_mapping, torch_module=_torch(),
+                            runtime=default_operator_runtime())
 
 
 def _execute_copy(
@@ -134,6 +154,7 @@ def _execute_copy(
     *,
     torch_module: Any,
     runtime: OperatorRuntime,
+    plan_key: Any = None,
 ) -> tuple[Any, Any]:
     op = COPY
     num_blocks, block_size, kv_heads, head_dim = _cache_shape(torch_module, key_cache, value_cache, op)
@@ -168,8 +189,26 @@ def _execute_copy(
         native_arguments=(key_cache, value_cache, block_mapping),
         fallback=lambda: kv_cache_copy_reference(torch_module, key_cache, value_cache, block_mapping),
         fallback_selected=FALLBACK_SELECTED,
+        plan_key=plan_key,
     )
     return _returned_caches(op, result, key_cache, value_cache)
+
+
+def _dispatch_copy(key_cache: Any, value_cache: Any, block_mapping: Any, *, torch_module: Any,
+                   runtime: OperatorRuntime) -> tuple[Any, Any]:
+    """A call shape validated before runs its kept plan; any other call takes ``_execute_copy``."""
+
+    plan_key = call_key(torch_module, COPY, (key_cache, value_cache, block_mapping))
+    plan = runtime.plan_for(plan_key)
+    if plan is None:
+        return _execute_copy(key_cache, value_cache, block_mapping, torch_module=torch_module, runtime=runtime,
+                             plan_key=plan_key)
+    result = runtime.run_plan(
+        plan, (key_cache, value_cache, block_mapping),
+        lambda: kv_cache_copy_reference(torch_module, key_cache, value_cache, block_mapping),
+        FALLBACK_SELECTED,
+    )
+    return _returned_caches(COPY, result, key_cache, value_cache)
 
 
 def kv_cache_copy(key_cache: Any, value_cache: Any, block_mapping: Any) -> tuple[Any, Any]:
@@ -180,5 +219,5 @@ def kv_cache_copy(key_cache: Any, value_cache: Any, block_mapping: Any) -> tuple
     place and returns them.
     """
 
-    return _execute_copy(key_cache, value_cache, block_mapping, torch_module=_torch(),
-                         runtime=default_operator_runtime())
+    return _dispatch_copy(key_cache, value_cache, block_mapping, torch_module=_torch(),
+                          runtime=default_operator_runtime())

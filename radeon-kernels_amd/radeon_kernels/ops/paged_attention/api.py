@@ -16,6 +16,7 @@ import math
 from typing import Any
 
 from radeon_kernels.ops._common import (
+    call_key,
     index_dtype_name,
     tensor_context,
     torch_runtime,
@@ -60,6 +61,7 @@ def _execute(
     *,
     torch_module: Any,
     runtime: OperatorRuntime,
+    plan_key: Any = None,
 ) -> Any:
     op = OPERATOR
     validate_tensor(torch_module, query, name="query", rank=3, operator=op)
@@ -120,7 +122,34 @@ def _execute(
         native_arguments=arguments,
         fallback=lambda: paged_attention_decode_reference(torch_module, *arguments),
         fallback_selected=FALLBACK_SELECTED,
+        plan_key=plan_key,
     )
+
+
+def _dispatch(
+    query: Any,
+    key_cache: Any,
+    value_cache: Any,
+    block_tables: Any,
+    context_lengths: Any,
+    scale: float | None,
+    *,
+    torch_module: Any,
+    runtime: OperatorRuntime,
+) -> Any:
+    """A call shape validated before runs its kept plan; any other call takes ``_execute``."""
+
+    # Only None and plain floats join the key: any other scale (int, bool, numpy) is validated.
+    key = call_key(torch_module, OPERATOR, (query, key_cache, value_cache, block_tables, context_lengths),
+                   scale) if scale is None or type(scale) is float else None
+    plan = runtime.plan_for(key)
+    if plan is not None:  # an equal call passed validation, so query is [B, Hq, D] and scale is valid
+        normalized = 1.0 / math.sqrt(query.shape[2]) if scale is None else scale
+        arguments = (query, key_cache, value_cache, block_tables, context_lengths, normalized)
+        return runtime.run_plan(plan, arguments, lambda: paged_attention_decode_reference(torch_module, *arguments),
+                                FALLBACK_SELECTED)
+    return _execute(query, key_cache, value_cache, block_tables, context_lengths, scale,
+                    torch_module=torch_module, runtime=runtime, plan_key=key)
 
 
 def paged_attention_decode(
@@ -138,7 +167,7 @@ def paged_attention_decode(
     in the query dtype.  ``scale`` defaults to ``1/sqrt(D)``.
     """
 
-    return _execute(
+    return _dispatch(
         query,
         key_cache,
         value_cache,

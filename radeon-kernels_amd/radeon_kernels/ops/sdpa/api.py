@@ -10,7 +10,7 @@ from __future__ import annotations
 import math
 from typing import Any
 
-from radeon_kernels.ops._common import tensor_context, torch_runtime, validate_same, validate_tensor
+from radeon_kernels.ops._common import call_key, tensor_context, torch_runtime, validate_same, validate_tensor
 from radeon_kernels.ops._runtime import OperatorRuntime, default_operator_runtime
 from radeon_kernels.ops.sdpa.reference import sdpa_fallback
 
@@ -37,7 +37,7 @@ def _normalize_scale(scale: float | None, head_dim: int) -> tuple[float, str]:
 
 
 def _execute(query: Any, key: Any, value: Any, is_causal: bool = False, scale: float | None = None, *,
-             torch_module: Any, runtime: OperatorRuntime) -> Any:
+             torch_module: Any, runtime: OperatorRuntime, plan_key: Any = None) -> Any:
     for name, tensor in (("query", query), ("key", key), ("value", value)):
         validate_tensor(torch_module, tensor, name=name, rank=4, operator=OPERATOR)
     validate_same(OPERATOR, query, key, first_name="query", second_name="key")
@@ -88,7 +88,26 @@ def _execute(query: Any, key: Any, value: Any, is_causal: bool = False, scale: f
         native_arguments=(query, key, value, is_causal, normalized_scale),
         fallback=lambda: sdpa_fallback(torch_module, query, key, value, is_causal, normalized_scale),
         fallback_selected=FALLBACK_SELECTED,
+        plan_key=plan_key,
     )
+
+
+def _dispatch(query: Any, key: Any, value: Any, is_causal: Any, scale: float | None, *, torch_module: Any,
+              runtime: OperatorRuntime) -> Any:
+    """A call shape validated before runs its kept plan; any other call takes ``_execute``."""
+
+    # is_causal joins the key only as a real bool and scale only as None or a plain float; any other
+    # value is validated.
+    plain = type(is_causal) is bool and (scale is None or type(scale) is float)
+    plan_key = call_key(torch_module, OPERATOR, (query, key, value), (is_causal, scale)) if plain else None
+    plan = runtime.plan_for(plan_key)
+    if plan is not None:  # an equal call passed validation: query is [B, Hq, S, D] and scale is valid
+        normalized = 1.0 / math.sqrt(query.shape[3]) if scale is None else scale
+        return runtime.run_plan(plan, (query, key, value, is_causal, normalized),
+                                lambda: sdpa_fallback(torch_module, query, key, value, is_causal, normalized),
+                                FALLBACK_SELECTED)
+    return _execute(query, key, value, is_causal, scale, torch_module=torch_module, runtime=runtime,
+                    plan_key=plan_key)
 
 
 def sdpa(query: Any, key: Any, value: Any, *, is_causal: bool = False, scale: float | None = None) -> Any:
@@ -98,4 +117,4 @@ def sdpa(query: Any, key: Any, value: Any, *, is_causal: bool = False, scale: fl
     sequence, head_dim]``; returns ``[batch, query_heads, sequence, head_dim]`` in the query dtype.
     """
 
-    return _execute(query, key, value, is_causal, scale, torch_module=_torch(), runtime=default_operator_runtime())
+    return _dispatch(query, key, value, is_causal, scale, torch_module=_torch(), runtime=default_operator_runtime())

@@ -7,7 +7,7 @@ parameters; a ``None`` return is an error.  The provider holds no operator-speci
 
 from __future__ import annotations
 
-from typing import Any, Mapping
+from typing import Any, Callable, Mapping
 
 from radeon_kernels.errors import RadeonKernelsError
 from radeon_kernels.runtime.loader import PrecompiledArtifactLoader
@@ -18,16 +18,25 @@ class NativeProviderError(RadeonKernelsError):
     """An approved native launch cannot be executed safely."""
 
 
+def resolve(loader: PrecompiledArtifactLoader, artifact: ArtifactSpec) -> Callable[..., Any]:
+    """The winner's callable, loaded (and digest-checked) through ``loader``."""
+
+    if artifact.provider != "native":
+        raise NativeProviderError(f"unsupported native winner provider: {artifact.provider!r}")
+    return loader.load_entrypoint(artifact).callable
+
+
+def invoke(entrypoint: Callable[..., Any], launch: Mapping[str, str | int | float | bool], *arguments: Any) -> Any:
+    result = entrypoint(*arguments, **launch)
+    if result is None:
+        raise NativeProviderError("native entrypoint returned no output")
+    return result
+
+
 def execute(
     loader: PrecompiledArtifactLoader,
     artifact: ArtifactSpec,
     launch: Mapping[str, str | int | float | bool],
     *arguments: Any,
 ) -> Any:
-    if artifact.provider != "native":
-        raise NativeProviderError(f"unsupported native winner provider: {artifact.provider!r}")
-    entrypoint = loader.load_entrypoint(artifact)
-    result = entrypoint.callable(*arguments, **dict(launch))
-    if result is None:
-        raise NativeProviderError("native entrypoint returned no output")
-    return result
+    return invoke(resolve(loader, artifact), dict(launch), *arguments)

@@ -43,6 +43,20 @@ EXPORTED_SYMBOLS = (
 PHASES = {"all": "rk_pa_decode", "partitions": "rk_pa_decode_partitions", "reduce": "rk_pa_decode_reduce"}
 
 
+def _repeatable(function: Any, args: tuple[Any, ...], check: Any, held: tuple[Any, ...]) -> Any:
+    """A zero-argument callable repeating ``function(*args)`` (``check`` raises on a non-zero status).
+
+    It keeps ``held`` -- the tensors the pointer arguments point into -- alive.
+    """
+
+    def launch(_held: tuple[Any, ...] = held) -> None:
+        status = function(*args)
+        if status:
+            check(status)
+
+    return launch
+
+
 class CabiError(RuntimeError):
     def __init__(self, status: int, message: str) -> None:
         self.status = status
@@ -99,28 +113,32 @@ class PagedAttentionLibrary:
         self.check(self.lib.rk_pa_decode_counter_words(batch, query_heads, kv_heads, ctypes.byref(out)))
         return int(out.value)
 
-    def decode_raw(self, *, query: int, key_cache: int, value_cache: int, block_tables: int, context_lengths: int,
-                   output: int, workspace: int, workspace_bytes: int, batch: int, query_heads: int, kv_heads: int,
-                   head_dim: int, num_blocks: int, block_size: int, max_blocks: int, scale: float, dtype: int,
-                   index_dtype: int, partition_tokens: int, variant: int, stream: int, phase: str = "all",
-                   counters: int = 0, counter_words: int = 0) -> int:
+    def _raw_call(self, *, query: int, key_cache: int, value_cache: int, block_tables: int, context_lengths: int,
+                  output: int, workspace: int, workspace_bytes: int, batch: int, query_heads: int, kv_heads: int,
+                  head_dim: int, num_blocks: int, block_size: int, max_blocks: int, scale: float, dtype: int,
+                  index_dtype: int, partition_tokens: int, variant: int, stream: int, phase: str = "all",
+                  counters: int = 0, counter_words: int = 0) -> tuple[Any, tuple[Any, ...]]:
+        """The C entry point of ``phase`` and its argument tuple."""
+
         head = (query, key_cache, value_cache, block_tables, context_lengths, output, workspace or None,
                 workspace_bytes)
         tail = (batch, query_heads, kv_heads, head_dim, num_blocks, block_size, max_blocks, ctypes.c_float(scale),
                 dtype, index_dtype, partition_tokens, variant, stream or None)
         if phase == "fused":
-            return self.lib.rk_pa_decode_fused(*head, counters or None, counter_words, *tail)
-        return getattr(self.lib, PHASES[phase])(*head, *tail)
+            return self.lib.rk_pa_decode_fused, (*head, counters or None, counter_words, *tail)
+        return getattr(self.lib, PHASES[phase]), (*head, *tail)
 
-    def decode(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
-               scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
-               out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
-               phase: str = "all", counters: Any | None = None) -> Any:
-        """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None).
+    def decode_raw(self, **arguments: Any) -> int:
+        """One launch on raw device pointers (the keywords of ``_raw_call``); returns the status."""
 
-        ``counters`` (phase ``"fused"`` only): an int32 tensor of at least ``counter_words`` zeros,
-        allocated zeroed here if None.
-        """
+        function, args = self._raw_call(**arguments)
+        return function(*args)
+
+    def _tensor_call(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
+                     scale: float | None, partition_tokens: int, variant: str, out: Any | None,
+                     workspace: Any | None, stream: Any | None, phase: str,
+                     counters: Any | None) -> tuple[Any, Any, tuple[Any, ...], tuple[Any, ...]]:
+        """(out, C function, its arguments, tensors those arguments point into)."""
 
         import torch
 
@@ -139,7 +157,7 @@ class PagedAttentionLibrary:
         if phase == "fused" and counters is None:
             counters = torch.zeros(self.counter_words(batch, query_heads, kv_heads), dtype=torch.int32,
                                    device=query.device)
-        status = self.decode_raw(
+        function, args = self._raw_call(
             query=query.data_ptr(), key_cache=key_cache.data_ptr(), value_cache=value_cache.data_ptr(),
             block_tables=block_tables.data_ptr(), context_lengths=context_lengths.data_ptr(), output=out.data_ptr(),
             workspace=workspace.data_ptr() if need else 0, workspace_bytes=workspace.numel() if need else 0,
@@ -151,8 +169,40 @@ class PagedAttentionLibrary:
             counters=counters.data_ptr() if counters is not None else 0,
             counter_words=counters.numel() if counters is not None else 0,
         )
-        self.check(status)
+        held = (query, key_cache, value_cache, block_tables, context_lengths, out, workspace, counters)
+        return out, function, args, held
+
+    def decode(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
+               scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
+               out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
+               phase: str = "all", counters: Any | None = None) -> Any:
+        """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None).
+
+        ``counters`` (phase ``"fused"`` only): an int32 tensor of at least ``counter_words`` zeros,
+        allocated zeroed here if None.
+        """
+
+        out, function, args, _ = self._tensor_call(query, key_cache, value_cache, block_tables, context_lengths,
+                                                   scale, partition_tokens, variant, out, workspace, stream, phase,
+                                                   counters)
+        self.check(function(*args))
         return out
+
+    def prepare(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
+                scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
+                out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
+                phase: str = "all", counters: Any | None = None) -> Any:
+        """The launch ``decode`` would make, with every argument converted once.
+
+        Returns a zero-argument callable that repeats it (one foreign call per launch, no Python
+        shape handling): what a timing loop needs to measure the GPU rather than this wrapper.  The
+        callable keeps the tensors it points into alive.
+        """
+
+        _, function, args, held = self._tensor_call(query, key_cache, value_cache, block_tables, context_lengths,
+                                                    scale, partition_tokens, variant, out, workspace, stream,
+                                                    phase, counters)
+        return _repeatable(function, args, self.check, held)
 
 
 _LIBRARY: PagedAttentionLibrary | None = None
@@ -208,54 +258,71 @@ class KvCacheLibrary:
         return self.lib.rk_kv_cache_append(key, value, key_cache, value_cache, slot_mapping, tokens, kv_heads,
                                            head_dim, num_blocks, block_size, dtype, index_dtype, stream or None)
 
-    def append(self, key: Any, value: Any, key_cache: Any, value_cache: Any, slot_mapping: Any, *,
-               stream: Any | None = None) -> tuple[Any, Any]:
-        """Launch on torch tensors (all on one GPU); writes the caches in place and returns them."""
+    def check(self, status: int) -> None:
+        if status != RK_KV_OK:
+            raise CabiError(status, self.last_error())
 
+    def _append_call(self, key: Any, value: Any, key_cache: Any, value_cache: Any, slot_mapping: Any,
+                     stream: Any | None) -> tuple[Any, tuple[Any, ...]]:
         import torch
 
         tokens, kv_heads, head_dim = (int(s) for s in key.shape)
         num_blocks, block_size = int(key_cache.shape[0]), int(key_cache.shape[1])
         if stream is None:
             stream = torch.cuda.current_stream(key.device)
-        status = self.append_raw(
-            key=key.data_ptr(), value=value.data_ptr(), key_cache=key_cache.data_ptr(),
-            value_cache=value_cache.data_ptr(), slot_mapping=slot_mapping.data_ptr(), tokens=tokens,
-            kv_heads=kv_heads, head_dim=head_dim, num_blocks=num_blocks, block_size=block_size,
-            dtype=RK_DTYPE_BF16 if key.dtype == torch.bfloat16 else RK_DTYPE_FP16,
-            index_dtype=RK_INDEX_INT64 if slot_mapping.dtype == torch.int64 else RK_INDEX_INT32,
-            stream=stream.cuda_stream,
-        )
-        if status != RK_KV_OK:
-            raise CabiError(status, self.last_error())
+        return self.lib.rk_kv_cache_append, (
+            key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.data_ptr(),
+            tokens, kv_heads, head_dim, num_blocks, block_size,
+            RK_DTYPE_BF16 if key.dtype == torch.bfloat16 else RK_DTYPE_FP16,
+            RK_INDEX_INT64 if slot_mapping.dtype == torch.int64 else RK_INDEX_INT32, stream.cuda_stream or None)
+
+    def append(self, key: Any, value: Any, key_cache: Any, value_cache: Any, slot_mapping: Any, *,
+               stream: Any | None = None) -> tuple[Any, Any]:
+        """Launch on torch tensors (all on one GPU); writes the caches in place and returns them."""
+
+        function, args = self._append_call(key, value, key_cache, value_cache, slot_mapping, stream)
+        self.check(function(*args))
         return key_cache, value_cache
 
+    def prepare_append(self, key: Any, value: Any, key_cache: Any, value_cache: Any, slot_mapping: Any, *,
+                       stream: Any | None = None) -> Any:
+        """``append``'s launch with its arguments converted once; calling the result repeats it."""
+
+        function, args = self._append_call(key, value, key_cache, value_cache, slot_mapping, stream)
+        return _repeatable(function, args, self.check, (key, value, key_cache, value_cache, slot_mapping))
 
     def copy_raw(self, *, key_cache: int, value_cache: int, block_mapping: int, pairs: int, num_blocks: int,
                  block_size: int, kv_heads: int, head_dim: int, dtype: int, index_dtype: int, stream: int) -> int:
         return self.lib.rk_kv_cache_copy(key_cache, value_cache, block_mapping, pairs, num_blocks, block_size,
                                          kv_heads, head_dim, dtype, index_dtype, stream or None)
 
-    def copy(self, key_cache: Any, value_cache: Any, block_mapping: Any, *, stream: Any | None = None
-             ) -> tuple[Any, Any]:
-        """Launch on torch tensors (all on one GPU); copies blocks in place and returns the caches."""
-
+    def _copy_call(self, key_cache: Any, value_cache: Any, block_mapping: Any,
+                   stream: Any | None) -> tuple[Any, tuple[Any, ...]]:
         import torch
 
         num_blocks, block_size, kv_heads, head_dim = (int(s) for s in key_cache.shape)
         if stream is None:
             stream = torch.cuda.current_stream(key_cache.device)
-        status = self.copy_raw(
-            key_cache=key_cache.data_ptr(), value_cache=value_cache.data_ptr(),
-            block_mapping=block_mapping.data_ptr(), pairs=int(block_mapping.shape[0]), num_blocks=num_blocks,
-            block_size=block_size, kv_heads=kv_heads, head_dim=head_dim,
-            dtype=RK_DTYPE_BF16 if key_cache.dtype == torch.bfloat16 else RK_DTYPE_FP16,
-            index_dtype=RK_INDEX_INT64 if block_mapping.dtype == torch.int64 else RK_INDEX_INT32,
-            stream=stream.cuda_stream,
-        )
-        if status != RK_KV_OK:
-            raise CabiError(status, self.last_error())
+        return self.lib.rk_kv_cache_copy, (
+            key_cache.data_ptr(), value_cache.data_ptr(), block_mapping.data_ptr(), int(block_mapping.shape[0]),
+            num_blocks, block_size, kv_heads, head_dim,
+            RK_DTYPE_BF16 if key_cache.dtype == torch.bfloat16 else RK_DTYPE_FP16,
+            RK_INDEX_INT64 if block_mapping.dtype == torch.int64 else RK_INDEX_INT32, stream.cuda_stream or None)
+
+    def copy(self, key_cache: Any, value_cache: Any, block_mapping: Any, *, stream: Any | None = None
+             ) -> tuple[Any, Any]:
+        """Launch on torch tensors (all on one GPU); copies blocks in place and returns the caches."""
+
+        function, args = self._copy_call(key_cache, value_cache, block_mapping, stream)
+        self.check(function(*args))
         return key_cache, value_cache
+
+    def prepare_copy(self, key_cache: Any, value_cache: Any, block_mapping: Any, *,
+                     stream: Any | None = None) -> Any:
+        """``copy``'s launch with its arguments converted once; calling the result repeats it."""
+
+        function, args = self._copy_call(key_cache, value_cache, block_mapping, stream)
+        return _repeatable(function, args, self.check, (key_cache, value_cache, block_mapping))
 
 
 _KV_LIBRARY: KvCacheLibrary | None = None
@@ -311,8 +378,12 @@ class SdpaLibrary:
         return self.lib.rk_sdpa_forward(query, key, value, output, batch, query_heads, kv_heads, sequence, head_dim,
                                         is_causal, ctypes.c_float(scale), dtype, stream or None)
 
-    def forward(self, query: Any, key: Any, value: Any, *, is_causal: bool = False, scale: float | None = None,
-                out: Any | None = None, stream: Any | None = None) -> Any:
+    def check(self, status: int) -> None:
+        if status != RK_SDPA_OK:
+            raise CabiError(status, self.last_error())
+
+    def _forward_call(self, query: Any, key: Any, value: Any, is_causal: bool, scale: float | None,
+                      out: Any | None, stream: Any | None) -> tuple[Any, Any, tuple[Any, ...]]:
         import torch
 
         batch, query_heads, sequence, head_dim = (int(s) for s in query.shape)
@@ -322,15 +393,23 @@ class SdpaLibrary:
             out = torch.empty_like(query)
         if stream is None:
             stream = torch.cuda.current_stream(query.device)
-        status = self.forward_raw(query=query.data_ptr(), key=key.data_ptr(), value=value.data_ptr(),
-                                  output=out.data_ptr(), batch=batch, query_heads=query_heads,
-                                  kv_heads=int(key.shape[1]), sequence=sequence, head_dim=head_dim,
-                                  is_causal=int(bool(is_causal)), scale=float(scale),
-                                  dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
-                                  stream=stream.cuda_stream)
-        if status != RK_SDPA_OK:
-            raise CabiError(status, self.last_error())
+        return out, self.lib.rk_sdpa_forward, (
+            query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), batch, query_heads, int(key.shape[1]),
+            sequence, head_dim, int(bool(is_causal)), ctypes.c_float(float(scale)),
+            RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16, stream.cuda_stream or None)
+
+    def forward(self, query: Any, key: Any, value: Any, *, is_causal: bool = False, scale: float | None = None,
+                out: Any | None = None, stream: Any | None = None) -> Any:
+        out, function, args = self._forward_call(query, key, value, is_causal, scale, out, stream)
+        self.check(function(*args))
         return out
+
+    def prepare_forward(self, query: Any, key: Any, value: Any, *, is_causal: bool = False,
+                        scale: float | None = None, out: Any | None = None, stream: Any | None = None) -> Any:
+        """``forward``'s launch with its arguments converted once; calling the result repeats it."""
+
+        out, function, args = self._forward_call(query, key, value, is_causal, scale, out, stream)
+        return _repeatable(function, args, self.check, (query, key, value, out))
 
 
 _SDPA_LIBRARY: SdpaLibrary | None = None

@@ -41,6 +41,7 @@
 #include <stdio.h>
 
 #include <string>
+#include <utility>
 
 #include "rk_sdpa.h"
 
@@ -52,8 +53,13 @@ constexpr int kThreads = kWave * kWaves;
 constexpr int kBlockM = 128;  // queries per workgroup (32 per wave)
 constexpr int kBlockN = 64;   // keys per block
 constexpr float kLog2e = 1.4426950408889634f;
+// How far (log2 units) the softmax reference may trail the running maximum before a rescale.
+constexpr float kRescaleSlack = 8.0f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -62,9 +68,9 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct Bf16 {
+  // Round to nearest even, both halves in one v_cvt_pk_bf16_f32.
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
   }
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
@@ -73,9 +79,9 @@ struct Bf16 {
 };
 
 struct Fp16 {
+  // Round to nearest even, both halves in one v_cvt_pk_f16_f32.
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
   }
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
@@ -108,17 +114,147 @@ struct Params {
   float scale_log2e;
 };
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt in bits [3:0] and [15:14], expcnt [6:4], lgkmcnt
+// [11:8]): all vector memory operations done, and all LDS operations done.
+constexpr int kWaitVmcnt0 = 0x0F70;
+constexpr int kWaitLgkmcnt0 = 0xC07F;
+
+// Keys per block: 64, or 32 for head_dim 256 so that two workgroups' double-buffered tiles fit in LDS.
+template <int D>
+struct Tiling {
+  static constexpr int kBlockN = D == 256 ? 32 : 64;
+  static constexpr int kRowBytes = D * 2;
+  static constexpr int kTileBytes = kBlockN * kRowBytes;  // one K or V tile
+  static constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;  // 1 KB per DMA instruction
+  static_assert(kDmaPerWave * 1024 * kWaves == kTileBytes, "tile must split into whole DMA instructions");
+};
+
+// LDS placement: 16-byte chunk c of tile row r sits in slot c ^ swizzle(r) of that row.  The
+// swizzle makes both LDS read patterns bank-conflict free: the K operand reads (16 consecutive rows,
+// one chunk) see 16 distinct slots (distinct bank groups once rows of 128 bytes pair up), and the
+// transposing V reads (4 consecutive rows, 4 consecutive chunks) see 16 distinct slots because the
+// swizzle of 4 consecutive rows differs in bits 2-3 (in bit 2 within each row parity for head_dim
+// 64, whose two rows share one 256-byte bank line).
+template <int D>
+__device__ __forceinline__ int swizzle(int r) {
+  if constexpr (D == 64)
+    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+}
+
+// global_load_lds_dwordx4: each lane's 16 bytes at `src` land in LDS at `lds_base` + 16 * lane
+// (`lds_base` wave-uniform); completion is tracked by the wave's vector memory counter.
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
+
+// Workgroup barrier that orders LDS accesses but leaves outstanding global loads (the next
+// block's DMA) in flight, unlike __syncthreads.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* ptr) {
+  typedef const __attribute__((address_space(3))) char lds_char;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)(ptr)));
+}
+
+// LDS reads issued as inline assembly with their own lgkmcnt wait.  The compiler places a vmcnt(0)
+// wait in front of every LDS read it emits while an LDS DMA is outstanding (it cannot tell which
+// bytes the DMA writes), which would stall on the next block's tiles; these reads only ever touch
+// the current block's buffer, whose DMA an explicit wait has already covered.  OFFSET (the buffer
+// and tile position, a compile-time constant) goes into the instruction's immediate offset field,
+// so each lane keeps only its swizzled per-k-step offsets in registers.
+template <int OFFSET>
+__device__ __forceinline__ void lds_read_b128_x4(u32x4 (&a)[4], const uint32_t* addr) {
+  static_assert(OFFSET >= 0 && OFFSET < 65536, "ds offset field");
+  __asm__ __volatile__(
+      "ds_read_b128 %0, %4 offset:%8\n\t"
+      "ds_read_b128 %1, %5 offset:%8\n\t"
+      "ds_read_b128 %2, %6 offset:%8\n\t"
+      "ds_read_b128 %3, %7 offset:%8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "i"(OFFSET)
+      : "memory");
+}
+
+// Transposing 64-bit reads for two 32-dim tiles of one 16-key k-step: rows r and r + 8 of each
+// tile form one MFMA A operand.
+template <int OFFSET>
+__device__ __forceinline__ void lds_read_tr_x2(u32x4 (&a)[2], const uint32_t* lo, const uint32_t* hi) {
+  static_assert(OFFSET >= 0 && OFFSET < 65536, "ds offset field");
+  u32x2 r[4];
+  __asm__ __volatile__(
+      "ds_read_b64_tr_b16 %0, %4 offset:%8\n\t"
+      "ds_read_b64_tr_b16 %1, %5 offset:%8\n\t"
+      "ds_read_b64_tr_b16 %2, %6 offset:%8\n\t"
+      "ds_read_b64_tr_b16 %3, %7 offset:%8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(lo[0]), "v"(hi[0]), "v"(lo[1]), "v"(hi[1]), "i"(OFFSET)
+      : "memory");
+  a[0] = u32x4{r[0][0], r[0][1], r[1][0], r[1][1]};
+  a[1] = u32x4{r[2][0], r[2][1], r[3][0], r[3][1]};
+}
+
+template <int OFFSET>
+__device__ __forceinline__ void lds_read_tr_x4(u32x4 (&a)[4], const uint32_t* lo, const uint32_t* hi) {
+  static_assert(OFFSET >= 0 && OFFSET < 65536, "ds offset field");
+  u32x2 r[8];
+  __asm__ __volatile__(
+      "ds_read_b64_tr_b16 %0, %8 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %1, %9 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %2, %10 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %3, %11 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %4, %12 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %5, %13 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %6, %14 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %7, %15 offset:%16\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(lo[0]), "v"(hi[0]), "v"(lo[1]), "v"(hi[1]), "v"(lo[2]), "v"(hi[2]), "v"(lo[3]), "v"(hi[3]),
+        "i"(OFFSET)
+      : "memory");
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = u32x4{r[2 * i][0], r[2 * i][1], r[2 * i + 1][0], r[2 * i + 1][1]};
+}
+
+template <int N>
+struct Int {
+  static constexpr int value = N;
+};
+
+// f(Int<0>{}), ..., f(Int<N - 1>{}): loop indices usable as constant expressions.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(Int<I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <class E, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(Params p) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
-  constexpr int KS = D / 16;                      // MFMA k-steps of S^T (16 dims each)
-  constexpr int DT = D / 32;                      // 32-dim tiles of O^T
-  constexpr int ROW = D + 8;                      // LDS row, elements (16-byte pad against bank conflicts)
-  constexpr int ROW_CHUNKS = D / 8;               // 16-byte chunks per row
-  constexpr int LOADS = kBlockN * ROW_CHUNKS / kThreads;  // chunks per thread per tensor per block
-  static_assert(LOADS * kThreads == kBlockN * ROW_CHUNKS, "tile must split evenly over the workgroup");
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBlockN * ROW];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kBlockN * ROW];
+  using T = Tiling<D>;
+  constexpr int BN = T::kBlockN;
+  constexpr int KS = D / 16;    // MFMA k-steps of S^T (16 dims each)
+  constexpr int DT = D / 32;    // 32-dim tiles of O^T
+  constexpr int ST = BN / 32;   // 32-key tiles of S^T per block
+  constexpr int PK = BN / 16;   // 16-key k-steps of O^T += V^T P^T per block
+  constexpr int RB = T::kRowBytes;
+  constexpr int TB = T::kTileBytes;
+  constexpr int NDMA = T::kDmaPerWave;
+  // Double-buffered K and V tiles, filled by DMA: the next block's loads run under this block's
+  // math.  Buffer u holds K at byte 2 u TB and V at (2 u + 1) TB.
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * TB];
+  static_assert(4 * TB <= 65536, "buffer offsets must fit the ds offset field");
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -141,6 +277,32 @@ __global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
   const uint16_t* __restrict__ kbase_ptr = p.k + static_cast<int64_t>(b * p.kv_heads + hkv) * S * D;
   const uint16_t* __restrict__ vbase_ptr = p.v + static_cast<int64_t>(b * p.kv_heads + hkv) * S * D;
 
+  const int kv_end = CAUSAL ? min(S, (qb + 1) * kBlockM) : S;
+  const int n_blocks = (kv_end + BN - 1) / BN;
+
+  // DMA sources: instruction i of this wave fills tile bytes [(wave * NDMA + i) KB, +1 KB); lane L
+  // lands at byte 16 L of it, i.e. row r, slot s, and fetches the row's chunk s ^ swizzle(r).
+  int dma_row[NDMA], dma_col[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int offset = (wave * NDMA + i) * 1024 + 16 * lane;
+    const int r = offset / RB, slot = (offset % RB) / 16;
+    dma_row[i] = r;
+    dma_col[i] = (slot ^ swizzle<D>(r)) * 8;
+  }
+  auto issue = [&](int kb0, int buffer) {
+    unsigned char* k_tile = lds + 2 * buffer * TB;
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      // Rows past the sequence re-read its last row (in bounds); their scores are masked and their
+      // V rows zeroed before use.
+      const int64_t offset = static_cast<int64_t>(min(kb0 + dma_row[i], S - 1)) * D + dma_col[i];
+      dma16(kbase_ptr + offset, k_tile + (wave * NDMA + i) * 1024);
+      dma16(vbase_ptr + offset, k_tile + TB + (wave * NDMA + i) * 1024);
+    }
+  };
+  issue(0, 0);  // in flight while Q is loaded
+
   // B operand of S^T = K Q^T: column = this lane's query, k-chunk (half) of 8 dims per k-step.
   u32x4 qB[KS];
 #pragma unroll
@@ -149,31 +311,33 @@ __global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
     qB[ks] = my_q < S ? value : u32x4{0, 0, 0, 0};
   }
 
-  const int kv_end = CAUSAL ? min(S, (qb + 1) * kBlockM) : S;
-  const int n_blocks = (kv_end + kBlockN - 1) / kBlockN;
-
-  // Staging of one K and one V block through registers: chunk c of this thread is row (tid + c*256) / ROW_CHUNKS.
-  u32x4 kreg[LOADS], vreg[LOADS];
-  auto load_block = [&](int kb) {
+  // Per-lane LDS byte offsets (from the start of a buffer's tile), one per k-step:
+  // K operand reads: row 32 t + col, chunk 2 ks + half (rows 32 apart share a swizzle; 32 t RB goes
+  // into the immediate offset).
+  const uint32_t lds0 = lds_address(lds);
+  uint32_t k_off[KS];
+  {
+    const int kswz = swizzle<D>(col);
 #pragma unroll
-    for (int c = 0; c < LOADS; ++c) {
-      const int chunk = tid + c * kThreads;
-      const int row = chunk / ROW_CHUNKS, part = chunk % ROW_CHUNKS;
-      const int key = kb * kBlockN + row;
-      const int64_t offset = static_cast<int64_t>(min(key, S - 1)) * D + part * 8;  // in bounds; masked later
-      kreg[c] = *reinterpret_cast<const u32x4*>(kbase_ptr + offset);
-      vreg[c] = key < S ? *reinterpret_cast<const u32x4*>(vbase_ptr + offset) : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto store_block = [&]() {
+    for (int ks = 0; ks < KS; ++ks) k_off[ks] = lds0 + col * RB + (((2 * ks + half) ^ kswz) << 4);
+  }
+  // Transposing V reads: lane L = 16g + j supplies row (key) 16 st + 8 r + 4 (g / 2) + j / 4 and
+  // columns 16 (g % 2) + 4 (j % 4) of each 32-column tile, so that it receives V[key][32 dt + L % 32]
+  // for the keys 16 st + 8 r + 4 (L / 32) + e, e = 0..3 -- the keys its P values cover.  Rows 16 apart
+  // share a swizzle (16 st RB goes into the immediate offset).
+  uint32_t v_lo[DT], v_hi[DT];
+  {
+    const int g = lane >> 4, j16 = lane & 15;
+    const int tr_row = 4 * (g >> 1) + (j16 >> 2);
+    const int tr_col = 16 * (g & 1) + 4 * (j16 & 3);  // element within the 32-column tile
+    const int swz_lo = swizzle<D>(tr_row), swz_hi = swizzle<D>(tr_row + 8);
+    const int chunk = tr_col >> 3, byte = (tr_col & 7) * 2;
 #pragma unroll
-    for (int c = 0; c < LOADS; ++c) {
-      const int chunk = tid + c * kThreads;
-      const int row = chunk / ROW_CHUNKS, part = chunk % ROW_CHUNKS;
-      *reinterpret_cast<u32x4*>(k_lds + row * ROW + part * 8) = kreg[c];
-      *reinterpret_cast<u32x4*>(v_lds + row * ROW + part * 8) = vreg[c];
+    for (int dt = 0; dt < DT; ++dt) {
+      v_lo[dt] = lds0 + TB + tr_row * RB + (((4 * dt + chunk) ^ swz_lo) << 4) + byte;
+      v_hi[dt] = lds0 + TB + (tr_row + 8) * RB + (((4 * dt + chunk) ^ swz_hi) << 4) + byte;
     }
-  };
+  }
 
   const float neg_inf = -__builtin_inff();
   f32x16 acc[DT];
@@ -182,57 +346,69 @@ __global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
   float m = neg_inf;   // running max of this lane's query (base-2 domain)
   float l_half = 0.f;  // running sum over the keys this half of the wave holds
 
-  // Transposing-read addresses: lane L = 16g + j supplies row (key) 16s + 8r + 4(g/2) + j/4 and
-  // columns 16(g%2) + 4(j%4) of each 32-column V tile, so that it receives V[key][32dt + L%32] for
-  // the keys 16s + 8r + 4(L/32) + e, e = 0..3 -- the keys its P values cover.
-  const int g = lane >> 4, j16 = lane & 15;
-  const int tr_row = 4 * (g >> 1) + (j16 >> 2);
-  const int tr_col = 16 * (g & 1) + 4 * (j16 & 3);
-
-  for (int nb = 0; nb < n_blocks; ++nb) {
-    load_block(nb);
-    __syncthreads();  // every wave is done with the previous block's LDS tiles
-    store_block();
-    __syncthreads();
-
-    const int kb0 = nb * kBlockN;
-    if (CAUSAL && kb0 > q_wave + 31) continue;  // no key of this block is visible to this wave
-
+  auto compute = [&](int kb0, auto buffer) {
+    constexpr int BUF = decltype(buffer)::value * 2 * TB;
     // S^T for keys kb0 + 32t + (8i + 4 half + r), r = 0..3, of this lane's query.
-    f32x16 s[2];
+    f32x16 s[ST];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s[t] = f32x16{};
-      const uint16_t* krow = k_lds + (t * 32 + col) * ROW + half * 8;
+    for (int t = 0; t < ST; ++t) s[t] = f32x16{};
+    // Four k-steps per LDS batch; the tiles' MFMA chains interleave, and each batch's reads are
+    // in flight while the previous batch's MFMAs execute.
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(krow + ks * 16);
-        s[t] = E::mfma(a, qB[ks], s[t]);
-      }
+    for (int ks = 0; ks < KS; ks += 4) {
+      static_for<ST>([&](auto tile) {
+        constexpr int t = decltype(tile)::value;
+        u32x4 a[4];
+        lds_read_b128_x4<BUF + t * 32 * RB>(a, k_off + ks);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[t] = E::mfma(a[i], qB[ks + i], s[t]);
+      });
     }
 
-    // Scale, mask, online softmax of this lane's query over the block.
-    const bool masked = (kb0 + kBlockN > S) || (CAUSAL && kb0 + kBlockN - 1 > q_wave);
-    float x[2][16];
+    // Mask (only the blocks that hold keys past the sequence or past a query of this wave: the test
+    // is wave-uniform, so the other blocks skip it), then the block maximum of this lane's query.
+    float x[ST][16];
+#pragma unroll
+    for (int t = 0; t < ST; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[t][r] = s[t][r];
+    if ((kb0 + BN > S) || (CAUSAL && kb0 + BN - 1 > q_wave)) {
+      const int key0 = kb0 + 4 * half;  // key of element (t, r) is key0 + 32 t + 8 (r / 4) + r % 4
+      const int limit = CAUSAL ? min(S - 1, my_q) : S - 1;
+#pragma unroll
+      for (int t = 0; t < ST; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (key0 + 32 * t + 8 * (r >> 2) + (r & 3) > limit) x[t][r] = neg_inf;
+    }
     float mx = neg_inf;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < ST; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb0 + 32 * t + 8 * (r >> 2) + 4 * half + (r & 3);
-        float value = s[t][r];
-        if (masked && (key >= S || (CAUSAL && key > my_q))) value = neg_inf;
-        x[t][r] = value;
-        mx = fmaxf(mx, value);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
     mx = max_halves(mx);
-    const float m_new = fmaxf(m, mx * p.scale_log2e);
-    const float m_use = m_new == neg_inf ? 0.f : m_new;  // a query with no visible key yet
-    const float alpha = fast_exp2(m - m_use);            // 0 while m = -inf
-    float psum = 0.f;
-    uint32_t pb[2][8];  // probabilities in the input dtype, B operands of the four PV k-steps
+
+    // Online softmax with a lagging reference: probabilities are exp2(x - m) for a reference m that
+    // may trail the true running maximum by up to kRescaleSlack, so they stay <= 2^kRescaleSlack
+    // (well inside fp16/bf16/fp32 range) and the sum and accumulator use the same reference, which
+    // the final division cancels.  m (and with it acc and the sum) moves only when some query's
+    // block maximum passes its reference by more than the slack -- in practice in the first blocks.
+    const float m_blk = mx * p.scale_log2e;
+    if (__builtin_amdgcn_ballot_w64(m_blk > m + kRescaleSlack)) {
+      const float m_new = fmaxf(m, m_blk);
+      const float alpha = m == neg_inf ? 0.f : fast_exp2(m - m_new);  // 1 where m did not move
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+      l_half *= alpha;
+      m = m_new;
+    }
+    const float m_use = m == neg_inf ? 0.f : m;  // a query with no visible key yet
+    float psum = 0.f;
+    uint32_t pb[ST][8];  // probabilities in the input dtype, B operands of the PV k-steps
+#pragma unroll
+    for (int t = 0; t < ST; ++t)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(fmaf(x[t][r], p.scale_log2e, -m_use));
@@ -240,30 +416,56 @@ __global__ __launch_bounds__(kThreads, 3) void sdpa_fwd_kernel(Params p) {
         psum += p0 + p1;
         pb[t][r >> 1] = E::pack(p0, p1);
       }
-    l_half = l_half * alpha + psum;
-    if (__builtin_amdgcn_ballot_w64(m_new != m)) {  // alpha == 1 in every lane leaves acc unchanged
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-    }
-    m = m_new;
+    l_half += psum;
 
-    // O^T += V^T P^T over four k-steps of 16 keys (k-step st covers keys 16 st .. 16 st + 15).
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int t = st >> 1, sub = st & 1;
+    // O^T += V^T P^T over the k-steps of 16 keys (k-step st covers keys 16 st .. 16 st + 15).
+    static_for<PK>([&](auto step) {
+      constexpr int st = decltype(step)::value;
+      constexpr int t = st >> 1, sub = st & 1;
       const u32x4 bop = {pb[t][4 * sub], pb[t][4 * sub + 1], pb[t][4 * sub + 2], pb[t][4 * sub + 3]};
+      constexpr int OFF = BUF + 16 * st * RB;
+      if constexpr (DT == 2) {
+        u32x4 a[2];
+        lds_read_tr_x2<OFF>(a, v_lo, v_hi);
+        acc[0] = E::mfma(a[0], bop, acc[0]);
+        acc[1] = E::mfma(a[1], bop, acc[1]);
+      } else {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const uint16_t* base = v_lds + (16 * st + tr_row) * ROW + 32 * dt + tr_col;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 8 * ROW));
-        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-        const u32x4 aop = {lo2[0], lo2[1], hi2[0], hi2[1]};
-        acc[dt] = E::mfma(aop, bop, acc[dt]);
+        for (int d4 = 0; d4 < DT; d4 += 4) {
+          u32x4 a[4];
+          lds_read_tr_x4<OFF>(a, v_lo + d4, v_hi + d4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[d4 + i] = E::mfma(a[i], bop, acc[d4 + i]);
+        }
       }
+    });
+  };
+
+  // One step: wait for this block's tiles (own DMA, then everyone's), start the next block's DMA
+  // into the other buffer (free: every wave has finished the previous block), compute.
+  auto step = [&](int nb, auto buffer) {
+    constexpr int U = decltype(buffer)::value;
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    lds_barrier();
+    const int kb0 = nb * BN;
+    if (nb + 1 < n_blocks) issue(kb0 + BN, 1 - U);
+    if (kb0 + BN > S) {
+      // Rows past the sequence hold copies of its last row: zero their V so that a non-finite value
+      // there cannot reach other queries through a zero probability.
+      constexpr int CHUNKS = TB / 16;
+      unsigned char* v_cur = lds + (2 * U + 1) * TB;
+      const int first = (S - kb0) * (RB / 16);
+#pragma unroll
+      for (int c = tid; c < CHUNKS; c += kThreads)
+        if (c >= first) *reinterpret_cast<u32x4*>(v_cur + 16 * c) = u32x4{0, 0, 0, 0};
+      lds_barrier();
     }
+    if (CAUSAL && kb0 > q_wave + 31) return;  // no key of this block is visible to this wave
+    compute(kb0, buffer);
+  };
+  for (int nb = 0; nb < n_blocks; nb += 2) {
+    step(nb, Int<0>{});
+    if (nb + 1 < n_blocks) step(nb + 1, Int<1>{});
   }
 
   // Normalise and store: lane holds O^T[32 dt + 8 i + 4 half + r][my_q], r = 0..3 contiguous dims.

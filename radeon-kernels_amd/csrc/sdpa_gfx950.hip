@@ -119,10 +119,17 @@ struct Params {
 constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr int kWaitLgkmcnt0 = 0xC07F;
 
-// Keys per block: 64, or 32 for head_dim 256 so that two workgroups' double-buffered tiles fit in LDS.
-template <int D>
+// Keys per block BN and workgroups per CU.  head_dim 256 takes 32-key blocks so that two workgroups'
+// double-buffered tiles fit in LDS.  head_dim 128 has two forms: 64-key blocks at two workgroups per
+// CU (fewer barriers: faster when the grid is at most one round of workgroups) and 32-key blocks at
+// three (more waves to overlap one another's softmax and MFMAs, and a finer causal diagonal: faster
+// on grids of several rounds).
+template <int D, int BN>
 struct Tiling {
-  static constexpr int kBlockN = D == 256 ? 32 : 64;
+  static_assert(BN == 32 || BN == 64, "32 or 64 keys per block");
+  static_assert(D != 256 || BN == 32, "head_dim 256 uses 32-key blocks");
+  static constexpr int kBlockN = BN;
+  static constexpr int kOccupancy = D == 128 && BN == 32 ? 3 : 2;
   static constexpr int kRowBytes = D * 2;
   static constexpr int kTileBytes = kBlockN * kRowBytes;  // one K or V tile
   static constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;  // 1 KB per DMA instruction
@@ -239,10 +246,10 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <class E, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(Params p) {
+template <class E, int D, int BLOCK_N, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, (Tiling<D, BLOCK_N>::kOccupancy)) void sdpa_fwd_kernel(Params p) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
-  using T = Tiling<D>;
+  using T = Tiling<D, BLOCK_N>;
   constexpr int BN = T::kBlockN;
   constexpr int KS = D / 16;    // MFMA k-steps of S^T (16 dims each)
   constexpr int DT = D / 32;    // 32-dim tiles of O^T
@@ -499,22 +506,28 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-template <class E, int D>
+// head_dim 128 grids above one round of three workgroups on each of the 256 CUs take the 32-key form.
+constexpr int64_t kWideGrid = 3 * 256;
+
+template <class E, int D, int BN>
 void launch_d(const Params& prm, bool causal, dim3 grid, hipStream_t stream) {
   if (causal)
-    hipLaunchKernelGGL((sdpa_fwd_kernel<E, D, true>), grid, dim3(kThreads), 0, stream, prm);
+    hipLaunchKernelGGL((sdpa_fwd_kernel<E, D, BN, true>), grid, dim3(kThreads), 0, stream, prm);
   else
-    hipLaunchKernelGGL((sdpa_fwd_kernel<E, D, false>), grid, dim3(kThreads), 0, stream, prm);
+    hipLaunchKernelGGL((sdpa_fwd_kernel<E, D, BN, false>), grid, dim3(kThreads), 0, stream, prm);
 }
 
 template <class E>
 void launch_e(const Params& prm, int64_t head_dim, bool causal, dim3 grid, hipStream_t stream) {
+  const int64_t workgroups = static_cast<int64_t>(grid.x) * grid.y;
   if (head_dim == 64)
-    launch_d<E, 64>(prm, causal, grid, stream);
+    launch_d<E, 64, 64>(prm, causal, grid, stream);
+  else if (head_dim == 128 && workgroups > kWideGrid)
+    launch_d<E, 128, 32>(prm, causal, grid, stream);
   else if (head_dim == 128)
-    launch_d<E, 128>(prm, causal, grid, stream);
+    launch_d<E, 128, 64>(prm, causal, grid, stream);
   else
-    launch_d<E, 256>(prm, causal, grid, stream);
+    launch_d<E, 256, 32>(prm, causal, grid, stream);
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }

@@ -101,6 +101,38 @@ def test_shapes_and_tails(gpu, sdpalib, shape, dtype):
     check(out.cpu(), q, k, v, causal, dtype, what=f"{shape}/{dtype}")
 
 
+# Grids of more than 768 workgroups (three rounds' worth on 256 CUs) run head_dim 128 in its 32-key
+# form; the shapes above all launch fewer.  B, Hq, Hkv, S, D, causal; workgroups = B * Hq * ceil(S / 128).
+WIDE = [
+    (4, 32, 8, 1024, 128, True),   # 1024 workgroups
+    (5, 64, 8, 300, 128, False),   # 960, ragged tail block
+    (3, 96, 12, 333, 128, True),   # 864, ragged, group of 8
+]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("shape", WIDE, ids=lambda s: "x".join(map(str, s)))
+def test_wide_grids(gpu, sdpalib, shape, dtype):
+    """Every head is computed; the oracle checks the first and last KV group of the first and last
+    sequence (the float64 oracle over all heads would take minutes)."""
+
+    import torch
+
+    b, hq, hkv, s, d, causal = shape
+    assert b * hq * -(-s // 128) > 768
+    q, k, v = make(torch, b, hq, hkv, s, d, dtype, seed=b * 7 + hq + s)
+    announce(f"sdpa wide grid {shape} {dtype}")
+    out = sdpalib.forward(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal).cpu()
+    group = hq // hkv
+    for batch in (0, b - 1):
+        for kv_head in (0, hkv - 1):
+            heads = slice(kv_head * group, (kv_head + 1) * group)
+            sl = slice(batch, batch + 1)
+            check(out[sl, heads], q[sl, heads], k[sl, kv_head:kv_head + 1], v[sl, kv_head:kv_head + 1], causal,
+                  dtype, what=f"{shape}/{dtype} sequence {batch} kv head {kv_head}")
+    assert torch.isfinite(out).all()
+
+
 def test_explicit_scale_and_large_logits(gpu, sdpalib):
     import torch
 

@@ -9,30 +9,31 @@
 // dispatch/sdpa-1.0.json); this is a flash-attention forward pass built for CDNA4:
 //
 //   sdpa_fwd_kernel  one 256-thread workgroup per (sequence, query head, block of 128 queries);
-//                    each of its 4 waves owns 32 queries and walks the keys in blocks of 64.  Per
-//                    block the workgroup stages K and V rows in LDS (row-major, rows padded by 16
-//                    bytes); every wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (K rows from
-//                    LDS as the A operand, its queries' Q^T held in registers as the B operand), so
-//                    each lane owns one query and 16 keys per 32-key tile and the softmax needs one
-//                    exchange between the two wave halves; the probabilities, rounded to the input
-//                    dtype, are already laid out as the B operand of O^T += V^T P^T, whose A operand
-//                    comes from ds_read_b64_tr_b16 transposing reads of the row-major V tile (the
-//                    keys of one MFMA k-step are taken in the order the S^T accumulator holds them,
-//                    which the transposing read reproduces by the addresses it is given).  The
-//                    accumulator is rescaled only when some lane's running maximum moved.  The
-//                    register budget is held to three workgroups per CU (at most 170 VGPRs), so one
-//                    workgroup's softmax and LDS traffic overlap another's MFMAs; K and V rows go
-//                    global -> registers -> LDS at the top of each block rather than being
-//                    prefetched a block ahead, which would cost the registers of the third
-//                    workgroup (measured: 1.3x slower on the long causal case).  With the causal
-//                    mask, blocks past a wave's last query are skipped and the grid runs the longest
-//                    query blocks of every head first (1.7x over head-major order on the long
+//                    each of its 4 waves owns 32 queries and walks the keys in blocks of BN (64, or
+//                    32 for head_dim 256 and for head_dim-128 grids of several rounds).  K and V
+//                    tiles reach LDS by DMA (global_load_lds_dwordx4, no staging registers),
+//                    double-buffered: block n + 1 loads while block n is computed, with one
+//                    LDS-only barrier per block.  Rows are unpadded and XOR-swizzled in 16-byte
+//                    chunks, which keeps both LDS read patterns free of bank conflicts.  Every wave
+//                    computes S^T = K Q^T with v_mfma_f32_32x32x16 (K rows from LDS as the A operand,
+//                    its queries' Q^T held in registers as the B operand), so each lane owns one
+//                    query and 16 keys per 32-key tile and the softmax needs one exchange between
+//                    the two wave halves; the probabilities, rounded to the input dtype, are already
+//                    laid out as the B operand of O^T += V^T P^T, whose A operand comes from
+//                    ds_read_b64_tr_b16 transposing reads of the row-major V tile (the keys of one
+//                    MFMA k-step are taken in the order the S^T accumulator holds them, which the
+//                    transposing read reproduces by the addresses it is given).  Masking runs only
+//                    on blocks that hold a masked key.  The softmax reference may lag the running
+//                    maximum by a bounded slack, so the accumulator is rescaled only when some
+//                    query's maximum outgrows it -- in practice in the first blocks.  With the
+//                    causal mask, blocks past a wave's last query are skipped and the grid runs the
+//                    longest query blocks of every head first (1.7x over head-major order on the long
 //                    causal case); without it, neighbouring query blocks of one head run together
 //                    and share its K and V rows in L2.
 //
 // Scores are kept in the base-2 domain: p = exp2((q . k) * scale * log2(e) - m), evaluated as one
-// fused multiply-add per score; the running maximum m is taken on the raw dot products (scale > 0
-// keeps their order) and scaled once per block.
+// fused multiply-add per score; the block maximum is taken on the raw dot products (scale > 0 keeps
+// their order) and scaled once per block.
 #include <hip/hip_runtime.h>
 
 #include <math.h>

@@ -120,8 +120,10 @@ struct Params {
 constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr int kWaitLgkmcnt0 = 0xC07F;
 
-// Keys per block BN and workgroups per CU.  head_dim 256 takes 32-key blocks so that two workgroups'
-// double-buffered tiles fit in LDS.  head_dim 128 has two forms: 64-key blocks at two workgroups per
+// Keys per block BN and workgroups per CU.  head_dim 256 takes 32-key blocks (its four tiles then stay
+// within the 64 KB the ds offset field addresses) at one workgroup per CU, whose 512 registers per
+// lane hold its accumulators without spilling (two per CU spilled and ran 5-9% slower).  head_dim
+// 128 has two forms: 64-key blocks at two workgroups per
 // CU (fewer barriers: faster when the grid is at most one round of workgroups) and 32-key blocks at
 // three (more waves to overlap one another's softmax and MFMAs, and a finer causal diagonal: faster
 // on grids of several rounds).
@@ -130,7 +132,7 @@ struct Tiling {
   static_assert(BN == 32 || BN == 64, "32 or 64 keys per block");
   static_assert(D != 256 || BN == 32, "head_dim 256 uses 32-key blocks");
   static constexpr int kBlockN = BN;
-  static constexpr int kOccupancy = D == 128 && BN == 32 ? 3 : 2;
+  static constexpr int kOccupancy = D == 256 ? 1 : (D == 128 && BN == 32 ? 3 : 2);
   static constexpr int kRowBytes = D * 2;
   static constexpr int kTileBytes = kBlockN * kRowBytes;  // one K or V tile
   static constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;  // 1 KB per DMA instruction

@@ -100,19 +100,22 @@ def public_call_us(torch, call, steps: int, batches: int = 5) -> float:
 SETTLE_SECONDS = 0.1
 
 
-def settle(torch, launch, seconds: float = SETTLE_SECONDS, limit: int = 100000) -> None:
-    """Untimed launches for at least ``seconds`` (at most ``limit`` of them) before the warmup steps.
+def settle(torch, launch, copies: int = 1, seconds: float = SETTLE_SECONDS, limit: int = 100000) -> None:
+    """Untimed launches for at least ``seconds`` (at most ``limit`` rounds) before the warmup steps.
 
     A few warmup steps of a microsecond-scale call leave the GPU's clocks still ramping when the timed
     region starts; the first timed region of the b1 decode then measured about 0.9 us per call slower
-    than an identical later one.
+    than an identical later one.  ``launch(i)`` runs on input copy ``i % copies``, rotating as the timed
+    loops do, so a kernel trace of the run averages one kind of launch.
     """
 
     torch.cuda.synchronize()
     start = time.perf_counter()
+    i = 0
     for _ in range(limit):
         for _ in range(10):
-            launch()
+            launch(i % copies)
+            i += 1
         torch.cuda.synchronize()
         if time.perf_counter() - start >= seconds:
             break
@@ -224,7 +227,7 @@ def main_sdpa(args) -> int:
     # Arguments converted once: one foreign call per launch, so small cases time the GPU.
     launch = lib.prepare_forward(q, k, v, is_causal=case.causal, scale=scale, out=out, stream=stream)
 
-    settle(torch, launch)
+    settle(torch, lambda _: launch())
     for _ in range(args.warmup):
         launch()
     torch.cuda.synchronize()
@@ -353,7 +356,7 @@ def main_kv(args) -> int:
     stream = torch.cuda.current_stream(device)
     # Arguments converted once per input set: one foreign call per launch, so the loop times the GPU.
     launches = [prepare(*inputs, stream=stream) for inputs in sets]
-    settle(torch, launches[0])
+    settle(torch, lambda i: launches[i](), copies)
     for i in range(args.warmup):
         launches[i % copies]()
     torch.cuda.synchronize()
@@ -526,7 +529,7 @@ def main(argv=None) -> int:
         prepared[phase, copy]()
 
     prepare(headline)
-    settle(torch, lambda: launch(headline, 0))
+    settle(torch, lambda i: launch(headline, i), copies)
     for i in range(args.warmup):
         launch(headline, i % copies)
     torch.cuda.synchronize()

@@ -155,6 +155,34 @@ def read_traffic(workload: str, variant: str, partition: int, merge: str = "redu
         return None
 
 
+def calibration_copy(torch, device) -> None:
+    """One 1 GiB device-to-device copy: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE readings
+    against the 1 GiB it is known to read and write give the counters' scale factors."""
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def read_case_traffic(summary: Path, workload: str):
+    """HBM bytes per kernel launch from a committed counter summary of one kv-cache or sdpa case, if
+    the summary's ``workload`` (operator, case and dtype) is exactly this run's."""
+
+    if not summary.is_file():
+        return None
+    fields = {}
+    for line in summary.read_text().splitlines():
+        if "=" in line and not line.lstrip().startswith("#"):
+            key, value = line.split("=", 1)
+            fields[key.strip()] = value.strip()
+    try:
+        return int(fields["hbm_bytes_per_launch"]) if fields.get("workload") == workload else None
+    except (KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(torch, data, seconds: float) -> dict:
     """Reference algorithm on the host cores over the first sequences of the workload."""
 
@@ -216,6 +244,8 @@ def main_sdpa(args) -> int:
         return 1
     device = torch.device("cuda:0")
     lib = sdpa_library()  # raises if the HIP library was not built
+    if args.calibration_copy:
+        calibration_copy(torch, device)
     cases = {**SDPA_CASES, **SDPA_LONG_CASES}
     case = cases[args.case or "b4-gqa32x8-s4096-d128-causal"]
     data = make_sdpa_inputs(case, dtype=args.dtype, device=device, generator_device=device)
@@ -285,7 +315,8 @@ def main_sdpa(args) -> int:
             "peak": MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(flops / (kernel_us * 1e6) / MFMA_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": read_case_traffic(ROOT / "profiles" / f"sdpa_fwd_kernel_{case.key}_traffic.txt",
+                                         f"sdpa-{case.key}-{args.dtype}"),
         },
         "rk_call": {"us_per_call": round(rk_us, 2), "selected": decision["selected"], "entry_id": decision["entry_id"]},
         "torch_sdpa_fallback_us": round(fallback_us, 2),
@@ -334,6 +365,8 @@ def main_kv(args) -> int:
         return 1
     device = torch.device("cuda:0")
     lib = kv_library()  # raises if the HIP library was not built
+    if args.calibration_copy:
+        calibration_copy(torch, device)
     if args.operator == "kv_cache_append":
         case = APPEND_CASES[args.case or "prefill-t128-mha32-d128-p32"]
         data = make_append_inputs(case, dtype=args.dtype, index_dtype="int64", device=device)
@@ -417,7 +450,8 @@ def main_kv(args) -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(moved / (kernel_us * 1e3) / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": read_case_traffic(ROOT / "profiles" / f"{kernel}_{case.key}.txt",
+                                         f"{args.operator}-{case.key}-{args.dtype}"),
         },
         "rk_call": {"us_per_call": round(rk_us, 2), "selected": decision["selected"], "entry_id": decision["entry_id"]},
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_kv(torch, args.operator, data, moved,
@@ -488,11 +522,7 @@ def main(argv=None) -> int:
     merge = args.merge or planned_merge
 
     if args.calibration_copy:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calibration_copy(torch, device)
 
     data = make_inputs(w, device=device, generator_device=device if w.ragged else "cpu")
     kv_bytes = data["kv_bytes"]

@@ -103,10 +103,14 @@ def test_shapes_and_tails(gpu, sdpalib, shape, dtype):
 
 # Grids of more than 768 workgroups (three rounds' worth on 256 CUs) run head_dim 128 in its 32-key
 # form; the shapes above all launch fewer.  B, Hq, Hkv, S, D, causal; workgroups = B * Hq * ceil(S / 128).
+# Sequence x KV head counts that divide into 8 take the XCD-owned grid order, the others the
+# two-dimensional ones.
 WIDE = [
-    (4, 32, 8, 1024, 128, True),   # 1024 workgroups
-    (5, 64, 8, 300, 128, False),   # 960, ragged tail block
-    (3, 96, 12, 333, 128, True),   # 864, ragged, group of 8
+    (4, 32, 8, 1024, 128, True),   # 1024 workgroups, 32 KV groups (XCD-owned)
+    (5, 64, 8, 300, 128, False),   # 960, ragged tail block, 40 KV groups (XCD-owned)
+    (3, 96, 12, 333, 128, True),   # 864, ragged, group of 8, 36 KV groups (two-dimensional)
+    (2, 32, 8, 1700, 64, True),    # 896, ragged, head_dim 64, 16 KV groups (XCD-owned)
+    (2, 16, 4, 3100, 256, False),  # 800, ragged, head_dim 256, 8 KV groups (XCD-owned)
 ]
 
 
@@ -131,6 +135,15 @@ def test_wide_grids(gpu, sdpalib, shape, dtype):
             check(out[sl, heads], q[sl, heads], k[sl, kv_head:kv_head + 1], v[sl, kv_head:kv_head + 1], causal,
                   dtype, what=f"{shape}/{dtype} sequence {batch} kv head {kv_head}")
     assert torch.isfinite(out).all()
+    # Every (sequence, head, query block) against torch's fp32 attention on the GPU (GQA expanded,
+    # contiguous operands): a grid order that skipped or repeated a block would fail here.
+    kk = k.to(gpu).repeat_interleave(group, dim=1).float().contiguous()
+    vv = v.to(gpu).repeat_interleave(group, dim=1).float().contiguous()
+    theirs = torch.nn.functional.scaled_dot_product_attention(q.to(gpu).float(), kk, vv, is_causal=causal,
+                                                              scale=1 / math.sqrt(d)).cpu()
+    error = (out.float() - theirs).abs()
+    assert (error <= CONTRACT_TOLERANCE + CONTRACT_TOLERANCE * theirs.abs()).all()
+    assert error.max().item() <= MAX_ABS[dtype]
 
 
 def test_explicit_scale_and_large_logits(gpu, sdpalib):

@@ -95,6 +95,27 @@ def test_bench_reads_traffic_only_for_its_exact_configuration(tmp_path, monkeypa
     assert bench.read_traffic("b128-x", "mfma", 2048) is None
 
 
+def test_case_traffic_matches_operator_case_and_dtype(tmp_path):
+    import bench
+
+    summary = tmp_path / "kv.txt"
+    summary.write_text("# measured\nworkload = kv_cache_copy-beam-pairs64-gqa8-d256-p16-bf16\n"
+                       "hbm_bytes_per_launch = 16839687\n")
+    assert bench.read_case_traffic(summary, "kv_cache_copy-beam-pairs64-gqa8-d256-p16-bf16") == 16_839_687
+    assert bench.read_case_traffic(summary, "kv_cache_copy-beam-pairs64-gqa8-d256-p16-fp16") is None
+    assert bench.read_case_traffic(tmp_path / "absent.txt", "anything") is None
+
+
+def test_committed_case_summaries_name_their_bench_workloads():
+    import bench
+
+    profiles = bench.ROOT / "profiles"
+    assert bench.read_case_traffic(profiles / "kv_append_kernel_prefill-t128-mha32-d128-p32.txt",
+                                   "kv_cache_append-prefill-t128-mha32-d128-p32-bf16") == 4_220_936
+    assert bench.read_case_traffic(profiles / "kv_copy_kernel_beam-pairs64-gqa8-d256-p16.txt",
+                                   "kv_cache_copy-beam-pairs64-gqa8-d256-p16-bf16") == 16_839_687
+
+
 def test_bench_uses_the_dispatch_table_launch():
     import bench
     from radeon_kernels import dispatch_plan

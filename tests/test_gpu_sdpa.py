@@ -111,6 +111,8 @@ WIDE = [
     (3, 96, 12, 333, 128, True),   # 864, ragged, group of 8, 36 KV groups (two-dimensional)
     (2, 32, 8, 1700, 64, True),    # 896, ragged, head_dim 64, 16 KV groups (XCD-owned)
     (2, 16, 4, 3100, 256, False),  # 800, ragged, head_dim 256, 8 KV groups (XCD-owned)
+    (32, 32, 8, 70, 128, True),    # 1024, one ragged query block per head, 256 KV groups (XCD-owned)
+    (64, 16, 8, 1, 64, False),     # 1024, S = 1, 512 KV groups (XCD-owned)
 ]
 
 

@@ -65,6 +65,10 @@ def parse_args(argv=None):
     parser.add_argument("--no-breakdown", action="store_true",
                         help="time only the headline call (no per-kernel breakdown of the other form)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--append", action="store_true",
+                        help="paged_attention_decode: also time one serving step that first appends each "
+                             "sequence's new token (position context_length - 1): kv_cache_append then the "
+                             "decode (two launches) against rk_pa_decode_append (one launch)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--calibration-copy", action="store_true",
                         help="run a 1 GiB device copy before timing (counter calibration under rocprofv3)")
@@ -153,6 +157,9 @@ def read_traffic(workload: str, variant: str, partition: int, merge: str = "redu
         return int(fields["hbm_bytes_per_launch"])
     except (KeyError, ValueError):
         return None
+
+
+PHASE_SYMBOL = {"all": "rk_pa_decode", "fused": "rk_pa_decode_fused"}
 
 
 def calibration_copy(torch, device) -> None:
@@ -623,6 +630,47 @@ def main(argv=None) -> int:
     decision = rk.get_last_dispatch()
     rk_us = public_call_us(torch, lambda: rk.paged_attention_decode(q, k, v, bt, cl), max(1, args.steps // 5))
 
+    step = None
+    if args.append:
+        # One decode step with its append, both forms, over the same rotating caches (the appends
+        # rewrite one slot per sequence of each copy; the decode timings above are already taken).
+        from radeon_kernels.cabi import kv_library
+
+        if variant != "mfma":
+            raise SystemExit("--append needs the mfma variant")
+        kvlib = kv_library()
+        gen = torch.Generator(device=device).manual_seed(data["seed"] + 1)
+        new_k = torch.randn((batch, hkv, d), generator=gen, device=device).to(q.dtype)
+        new_v = torch.randn((batch, hkv, d), generator=gen, device=device).to(q.dtype)
+        pos = cl.long().clamp(max=mb * bs) - 1
+        safe = pos.clamp(min=0)
+        slots = torch.where(pos >= 0, bt.long().gather(1, (safe // bs).unsqueeze(1)).squeeze(1) * bs + safe % bs,
+                            torch.full_like(pos, -1))
+        appends = [kvlib.prepare_append(new_k, new_v, kc, vc, slots, stream=stream) for kc, vc in caches]
+        fused_steps = [lib.prepare(q, kc, vc, bt, cl, partition_tokens=partition, variant=variant, out=out,
+                                   workspace=workspace, stream=stream, phase=headline, counters=counters,
+                                   new_key=new_k, new_value=new_v) for kc, vc in caches]
+
+        def step_us(one_step) -> float:
+            for i in range(args.warmup):
+                one_step(i % copies)
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for i in range(args.steps):
+                one_step(i % copies)
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t) / args.steps * 1e6
+
+        def two_launches(i: int) -> None:
+            appends[i]()
+            launch(headline, i)
+
+        two = step_us(two_launches)
+        one = step_us(lambda i: fused_steps[i]())
+        step = {"append_tokens": int(batch), "us_per_step_two_launch": round(two, 2),
+                "us_per_step_one_launch": round(one, 2), "entrypoints": ["rk_kv_cache_append + " + PHASE_SYMBOL[headline],
+                                                                         "rk_pa_decode_append"]}
+
     traffic = read_traffic(w.name, variant, partition, merge)
     result = {
         "metric": METRIC,
@@ -666,6 +714,8 @@ def main(argv=None) -> int:
     }
     if hot is not None:
         result["us_per_call_cache_resident"] = hot
+    if step is not None:
+        result["decode_step_with_append"] = step
     result["rk_call"] = {"us_per_call": round(rk_us, 2), "selected": decision["selected"],
                          "entry_id": decision["entry_id"], "cache_resident": copies > 1}
     if not args.no_cpu_baseline:

@@ -19,6 +19,10 @@
  *                           -> no reference counterpart: the single-launch form of rk_pa_decode for
  *                              callers that keep a small persistent counter buffer per stream
  *                              (the torch extension does).
+ *   rk_pa_decode_append    -> no reference counterpart: kv_cache_append of each sequence's new token
+ *                              (benchmarks/kv_cache/native_kv_cache.hip:22-51, one token per
+ *                              sequence at position context_length - 1) followed by rk_pa_decode, in
+ *                              the decode's own launch.
  *   rk_pa_last_error, rk_pa_version
  *                           -> error text that TORCH_CHECK carried in the reference
  *                              (native_paged_attention.hip:199-219,239-240).
@@ -142,6 +146,32 @@ int rk_pa_decode_fused(const void* query, const void* key_cache, const void* val
                        int64_t head_dim, int64_t num_blocks, int64_t block_size,
                        int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
                        int64_t partition_tokens, int variant, void* stream);
+
+/*
+ * Append-and-decode (no reference counterpart): one decode step of a serving loop in the decode's
+ * launch.  Each sequence b has one new token at position context_lengths[b] - 1 (context lengths
+ * already count it), i.e. in slot block_tables[b, t / block_size] * block_size + t % block_size.
+ * The call stores new_key[b] / new_value[b] ([batch, kv_heads, head_dim], the dtype of the caches)
+ * into that slot of key_cache / value_cache, exactly as kv_cache_append with that slot mapping
+ * would, and attends over the context with the new token read from new_key / new_value: outputs
+ * and caches are bit-identical to the append followed by rk_pa_decode (or rk_pa_decode_fused).
+ *
+ * Preconditions beyond rk_pa_decode's: no other sequence of the call attends to a new token's slot
+ * (each new token lies in its own sequence's tail block, as paged serving allocates them).  A
+ * context length <= 0 appends nothing; a new token whose block id is outside [0, num_blocks) is not
+ * stored and is masked, as the append and the decode each treat it.
+ *
+ * counters/counter_words: NULL for the two-launch form (partition kernel, then the reduce kernel
+ * when a sequence can span several partitions), or the counters of rk_pa_decode_fused for the
+ * single-launch form.  variant: RK_PA_VARIANT_MFMA only (RK_ERR_UNSUPPORTED otherwise).
+ */
+int rk_pa_decode_append(const void* query, const void* new_key, const void* new_value, void* key_cache,
+                        void* value_cache, const void* block_tables, const void* context_lengths,
+                        void* output, void* workspace, size_t workspace_bytes, uint32_t* counters,
+                        size_t counter_words, int64_t batch, int64_t query_heads, int64_t kv_heads,
+                        int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                        int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
+                        int64_t partition_tokens, int variant, void* stream);
 
 /* Text describing the last non-RK_OK status returned on the calling thread. */
 const char* rk_pa_last_error(void);

@@ -249,6 +249,13 @@ struct Params {
   // Fused merge only (else null): [batch, kv_heads * head_chunks] arrival counters, zero on entry,
   // left zero on exit (the last arriver resets its counter).
   uint32_t* __restrict__ counters;
+  // Append-and-decode only (else null): [batch, kv_heads, D] K and V rows of each sequence's new
+  // token (position context_length - 1).  The kernel attends to them from these buffers and stores
+  // them into that position's cache slot; k_store / v_store are the caches' base addresses.
+  const uint16_t* __restrict__ new_k;
+  const uint16_t* __restrict__ new_v;
+  uint16_t* k_store;
+  uint16_t* v_store;
   int64_t block_stride;        // elements between physical blocks: BS * Hkv * D
   int64_t row_stride;          // elements between slots of a block: Hkv * D
   int32_t batch;
@@ -401,6 +408,11 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
 //   QK_MFMA QK^T on MFMA (true) or on fp32 FMAs + DPP row sums (false)
 //   UB      block_size >= 16: every 16-aligned tile lies inside one cache block, so the block id is
 //           wave-uniform and addresses are a scalar base plus fixed 32-bit per-lane offsets
+//   AP      append-and-decode: each sequence's new token (position ctx - 1) is read from new_k /
+//           new_v instead of the cache, and the workgroup whose partition holds it (head chunk 0)
+//           stores its KV head's rows into the token's cache slot.  No other workgroup of the launch
+//           reads that slot (its block belongs to this sequence's tail), so nothing waits for the
+//           store; the next launch sees it.  MFMA variant only.
 //
 // MFMA variant data path per 16-token tile and wave:
 //   K: global_load_lds_dwordx4 straight into a per-wave LDS slot.  Each DMA instruction moves
@@ -411,8 +423,9 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
 //   Pipeline: DEPTH tiles are in flight ahead of the one being computed (DEPTH + 1 register tiles
 //   and LDS K slots rotate).  Step n: wait until tile n has landed -> issue tile n + DEPTH ->
 //   read K(n) from LDS -> MFMA -> softmax -> PV(n).
-template <class E, int D, int GC, bool QK_MFMA, bool UB>
+template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP>
 __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
+  static_assert(!AP || QK_MFMA, "append-and-decode is built for the MFMA variant");
   constexpr int KSTEPS = D / 32;       // MFMA k-steps; also DMA instructions per K tile
   constexpr int VEC = D / 16;          // elements of a token row per lane (row = 16 lanes)
   constexpr int VW = VEC / 2;          // 32-bit words per lane per token row
@@ -506,6 +519,17 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     if (idx < slice) ids[i] = load_raw_index(p.block_tables, table_row + idx, is64);
   }
 
+  // Append: wave 0 lanes [0, CPR) hold one 16-byte chunk of the new token's K row of this KV head,
+  // lanes [CPR, 2 CPR) of its V row, loaded with the prologue.
+  const int64_t new_row = (static_cast<int64_t>(b) * p.kv_heads + kvh) * D;
+  u32x4 ap_chunk = {0u, 0u, 0u, 0u};
+  if constexpr (AP) {
+    if (wave == 0 && lane < 2 * CPR) {
+      const uint16_t* src = (lane < CPR ? p.new_k : p.new_v) + new_row + (lane % CPR) * 8;
+      ap_chunk = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+    }
+  }
+
   // Query operands.
   const int64_t q_row0 = static_cast<int64_t>(b) * p.query_heads + head0;
   const int my_head = j % GC;  // head of the scores this lane holds
@@ -569,6 +593,9 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     return;
   }
   const int p_end = static_cast<int>(min(static_cast<int64_t>(p0 + P), ctx));
+  // Append: the new token's position, and whether this partition holds it (the last one does).
+  const int ap_pos = static_cast<int>(ctx - 1);
+  const bool ap_here = AP && ap_pos >= p0 && ap_pos < p_end;
 
   // Stage this partition's block-table slice in LDS (-1 marks ids outside [0, num_blocks)).  It is
   // made visible by the barrier in front of the main loop.
@@ -654,6 +681,26 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
       tile.valid = 0;
 #pragma unroll
       for (int r = 0; r < 4; ++r) tile.valid |= (block_ok && t0 + 4 * g + r < p_end) ? (1u << r) : 0u;
+      if constexpr (AP) {
+        // The new token's tile (a wave-uniform branch, taken once per sequence and KV head): its row
+        // comes from new_k / new_v through per-lane address selects.  It issues the same loads in the
+        // same order as the common path below, which keeps its scalar-base addressing.
+        if (ap_here && ap_pos >= t0 && ap_pos < t0 + kTile) {
+          u32x4* dst = s_k + slot * KTILE16;
+#pragma unroll
+          for (int n = 0; n < KSTEPS; ++n) {
+            const int row = RPI * n + dma_row;
+            const uint16_t* src = t0 + row == ap_pos ? p.new_k + new_row + ((dma_pos ^ (row & SWZ)) << 3)
+                                                     : kbase + base + kdma_off[n];
+            dma_to_lds16(src, dst + n * kWave);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            vrow[r] = t0 + 4 * g + r == ap_pos ? p.new_v + new_row + j * VEC : vbase + base + v_lane_off[r];
+          load_v_rows(tile.v, vrow);
+          return;
+        }
+      }
       if constexpr (QK_MFMA) {
         const uint16_t* kb = kbase + base;
         u32x4* dst = s_k + slot * KTILE16;
@@ -676,6 +723,9 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
           const int row = RPI * n + dma_row;
           const int t = t0 + row;
           const uint16_t* src = kbase + row_base(block_of(t), t) + ((dma_pos ^ (row & SWZ)) << 3);
+          if constexpr (AP) {
+            if (ap_here && t == ap_pos) src = p.new_k + new_row + ((dma_pos ^ (row & SWZ)) << 3);
+          }
           dma_to_lds16(src, dst + n * kWave);
         }
       }
@@ -686,6 +736,9 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
         tile.valid |= (t < p_end && pb >= 0) ? (1u << r) : 0u;
         vrow[r] = vbase + row_base(pb, t) + j * VEC;
         krow[r] = kbase + row_base(pb, t) + j * VEC;
+        if constexpr (AP) {
+          if (ap_here && t == ap_pos) vrow[r] = p.new_v + new_row + j * VEC;
+        }
       }
     }
     if constexpr (!QK_MFMA) load_v_rows(tile.kr, krow);  // K rows of masked tokens need no zeroing
@@ -863,6 +916,20 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     }
   }
   lds_barrier();
+  if constexpr (AP) {
+    // The new token's rows into its cache slot (skipped, like the append operator, when its block id
+    // is invalid).  Fire and forget: no wave of this launch reads the slot, and the explicit memory
+    // waits below stay exact (a store issued before a tile's loads only makes them wait longer).
+    if (ap_here && chunk == 0 && wave == 0 && lane < 2 * CPR) {
+      const int pb = s_table[(ap_pos >> lb) - blk0];
+      if (pb >= 0) {
+        uint16_t* dst = (lane < CPR ? p.k_store : p.v_store) + static_cast<int64_t>(pb) * p.block_stride +
+                        static_cast<int64_t>(ap_pos & bs_mask) * p.row_stride + static_cast<int64_t>(kvh) * D +
+                        (lane % CPR) * 8;
+        *reinterpret_cast<u32x4*>(dst) = ap_chunk;
+      }
+    }
+  }
   if constexpr (!UB) {
     if (n_tiles > 0) issue_tile(ta, 0, t0_of(0));
   }
@@ -1064,23 +1131,25 @@ int64_t counter_words_for(int64_t batch, int64_t query_heads, int64_t kv_heads) 
   return batch * kv_heads * ((group + gc - 1) / gc);
 }
 
-template <class E, int D, int GC, bool QK_MFMA>
+template <class E, int D, int GC, bool QK_MFMA, bool AP>
 void launch_partition_ub(const Params& prm, int64_t grid, hipStream_t stream) {
   if (prm.bs_log2 >= 4) {
-    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, true>),
+    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, true, AP>),
                        dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, prm);
   } else {
-    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, false>),
+    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, false, AP>),
                        dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, prm);
   }
 }
 
 template <class E, int D, int GC>
 hipError_t launch_partition(const Params& prm, int variant, int64_t grid, hipStream_t stream) {
-  if (variant == RK_PA_VARIANT_MFMA)
-    launch_partition_ub<E, D, GC, true>(prm, grid, stream);
+  if (prm.new_k != nullptr)
+    launch_partition_ub<E, D, GC, true, true>(prm, grid, stream);  // validated: MFMA variant
+  else if (variant == RK_PA_VARIANT_MFMA)
+    launch_partition_ub<E, D, GC, true, false>(prm, grid, stream);
   else
-    launch_partition_ub<E, D, GC, false>(prm, grid, stream);
+    launch_partition_ub<E, D, GC, false, false>(prm, grid, stream);
   return hipGetLastError();
 }
 
@@ -1144,6 +1213,7 @@ namespace {
 constexpr int kPhasePartitions = 1;
 constexpr int kPhaseReduce = 2;
 constexpr int kPhaseFused = 4;  // partition kernel merging in its last workgroups; no reduce launch
+constexpr int kPhaseAppend = 8; // partition kernel also writes each sequence's new token (AP)
 
 int decode_phases(const void* query, const void* key_cache, const void* value_cache,
                   const void* block_tables, const void* context_lengths, void* output, void* workspace,
@@ -1151,9 +1221,17 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
                   int64_t head_dim, int64_t num_blocks, int64_t block_size,
                   int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
                   int64_t partition_tokens, int variant, void* stream, int phases,
-                  uint32_t* counters = nullptr, size_t counter_words = 0) {
+                  uint32_t* counters = nullptr, size_t counter_words = 0,
+                  const void* new_key = nullptr, const void* new_value = nullptr) {
   if (!query || !key_cache || !value_cache || !block_tables || !context_lengths || !output)
     return fail(RK_ERR_INVALID_ARGUMENT, "tensor pointers must not be NULL");
+  const bool append = (phases & kPhaseAppend) != 0;
+  if (append && (!new_key || !new_value))
+    return fail(RK_ERR_INVALID_ARGUMENT, "new_key and new_value must not be NULL");
+  if (append && variant != RK_PA_VARIANT_MFMA)
+    return fail(RK_ERR_UNSUPPORTED, "append-and-decode is built for RK_PA_VARIANT_MFMA only");
+  if (append && (!aligned16(new_key) || !aligned16(new_value)))
+    return fail(RK_ERR_UNSUPPORTED, "new_key and new_value must be 16-byte aligned");
   if (dtype != RK_DTYPE_FP16 && dtype != RK_DTYPE_BF16)
     return fail(RK_ERR_INVALID_ARGUMENT, "dtype must be RK_DTYPE_FP16 or RK_DTYPE_BF16");
   if (index_dtype != RK_INDEX_INT32 && index_dtype != RK_INDEX_INT64)
@@ -1209,6 +1287,12 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
     prm.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes_for(s));
   }
   prm.counters = fused ? counters : nullptr;
+  if (append) {
+    prm.new_k = static_cast<const uint16_t*>(new_key);
+    prm.new_v = static_cast<const uint16_t*>(new_value);
+    prm.k_store = static_cast<uint16_t*>(const_cast<void*>(key_cache));
+    prm.v_store = static_cast<uint16_t*>(const_cast<void*>(value_cache));
+  }
   prm.block_stride = block_size * kv_heads * head_dim;
   prm.row_stride = kv_heads * head_dim;
   prm.batch = static_cast<int32_t>(batch);
@@ -1292,6 +1376,23 @@ extern "C" int rk_pa_decode_fused(const void* query, const void* key_cache, cons
                        workspace, workspace_bytes, batch, query_heads, kv_heads, head_dim,
                        num_blocks, block_size, max_blocks_per_sequence, scale, dtype, index_dtype,
                        partition_tokens, variant, stream, kPhaseFused, counters, counter_words);
+}
+
+extern "C" int rk_pa_decode_append(const void* query, const void* new_key, const void* new_value,
+                                   void* key_cache, void* value_cache, const void* block_tables,
+                                   const void* context_lengths, void* output, void* workspace,
+                                   size_t workspace_bytes, uint32_t* counters, size_t counter_words,
+                                   int64_t batch, int64_t query_heads, int64_t kv_heads,
+                                   int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                                   int64_t max_blocks_per_sequence, float scale, int dtype,
+                                   int index_dtype, int64_t partition_tokens, int variant,
+                                   void* stream) {
+  const int phases = kPhaseAppend | (counters != nullptr ? kPhaseFused : kPhasePartitions | kPhaseReduce);
+  return decode_phases(query, key_cache, value_cache, block_tables, context_lengths, output,
+                       workspace, workspace_bytes, batch, query_heads, kv_heads, head_dim,
+                       num_blocks, block_size, max_blocks_per_sequence, scale, dtype, index_dtype,
+                       partition_tokens, variant, stream, phases, counters, counter_words, new_key,
+                       new_value);
 }
 
 extern "C" const char* rk_pa_last_error(void) { return g_last_error.c_str(); }

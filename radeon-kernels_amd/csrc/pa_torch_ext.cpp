@@ -20,6 +20,10 @@
 // for the next call on that stream.  Calls made while the stream is being captured into a graph
 // always use the two-launch form, which needs no state that outlives the call.
 //
+// decode_append_mfma (no reference counterpart) is one serving step in the decode's launch: it
+// stores each sequence's new token (position context_length - 1) into the caches in place and
+// returns the decode of the updated context, bit-identical to kv_cache_append then decode_mfma.
+//
 // The kernels (pa_decode_gfx950.hip) are linked into this module, so it depends on no other file
 // of the pack and the digest a dispatch entry pins for it covers the kernels it runs.
 #include <torch/extension.h>
@@ -93,10 +97,13 @@ bool fused_merge_requested(const std::string& merge, int64_t items) {
   return items < kFusedMergeMaxItems;
 }
 
+// new_key / new_value: undefined for a plain decode; for append-and-decode the [batch, kv_heads,
+// head_dim] rows of each sequence's new token (rk_pa_decode_append).
 at::Tensor decode(const at::Tensor& query, const at::Tensor& key_cache,
                   const at::Tensor& value_cache, const at::Tensor& block_tables,
                   const at::Tensor& context_lengths, double scale, int64_t partition_tokens,
-                  const std::string& merge, int variant) {
+                  const std::string& merge, int variant, const at::Tensor& new_key = at::Tensor(),
+                  const at::Tensor& new_value = at::Tensor()) {
   check_data(query, "query", 3);
   check_data(key_cache, "key_cache", 4);
   check_data(value_cache, "value_cache", 4);
@@ -122,6 +129,19 @@ at::Tensor decode(const at::Tensor& query, const at::Tensor& key_cache,
                         !value_cache.requires_grad(),
                     "paged attention decode is inference-only");
 
+  const bool append = new_key.defined();
+  if (append) {
+    check_data(new_key, "new_key", 3);
+    check_data(new_value, "new_value", 3);
+    TORCH_CHECK_VALUE(new_key.device() == device && new_value.device() == device,
+                      "all tensors must be on the query device");
+    TORCH_CHECK_TYPE(new_key.scalar_type() == query.scalar_type() &&
+                         new_value.scalar_type() == query.scalar_type(),
+                     "new_key, new_value and query dtypes must match");
+    TORCH_CHECK_VALUE(new_key.sizes() == new_value.sizes() && new_key.size(0) == query.size(0) &&
+                          new_key.size(1) == key_cache.size(2) && new_key.size(2) == key_cache.size(3),
+                      "new_key and new_value must have shape [batch, kv_heads, head_dim]");
+  }
   const int64_t batch = query.size(0);
   const int64_t query_heads = query.size(1);
   const int64_t head_dim = query.size(2);
@@ -151,7 +171,17 @@ at::Tensor decode(const at::Tensor& query, const at::Tensor& key_cache,
   if (status != RK_OK) raise_status(status);
   const int64_t partitions = (max_blocks * block_size + partition_tokens - 1) / partition_tokens;
   const bool fused = fused_merge_requested(merge, static_cast<int64_t>(words) * partitions);
-  if (fused && workspace_bytes > 0 && !capturing(stream)) {
+  if (append) {
+    uint32_t* counters = fused && workspace_bytes > 0 && !capturing(stream) ? stream_counters(query, stream, words)
+                                                                            : nullptr;
+    status = rk_pa_decode_append(query.data_ptr(), new_key.data_ptr(), new_value.data_ptr(),
+                                 key_cache.data_ptr(), value_cache.data_ptr(), block_tables.data_ptr(),
+                                 context_lengths.data_ptr(), output.data_ptr(), workspace_ptr,
+                                 workspace_bytes, counters, counters != nullptr ? words : 0, batch,
+                                 query_heads, kv_heads, head_dim, num_blocks, block_size, max_blocks,
+                                 static_cast<float>(scale), dtype, index_dtype, partition_tokens, variant,
+                                 stream);
+  } else if (fused && workspace_bytes > 0 && !capturing(stream)) {
     uint32_t* counters = stream_counters(query, stream, words);
     status = rk_pa_decode_fused(query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
                                 block_tables.data_ptr(), context_lengths.data_ptr(), output.data_ptr(),
@@ -186,6 +216,17 @@ at::Tensor decode_valu(const at::Tensor& query, const at::Tensor& key_cache,
                 partition_tokens, merge, RK_PA_VARIANT_VALU);
 }
 
+// Append-and-decode: writes each sequence's new token into the caches (in place) and returns the
+// decode of the updated context, as kv_cache_append followed by decode_mfma would.
+at::Tensor decode_append_mfma(const at::Tensor& query, const at::Tensor& new_key,
+                              const at::Tensor& new_value, const at::Tensor& key_cache,
+                              const at::Tensor& value_cache, const at::Tensor& block_tables,
+                              const at::Tensor& context_lengths, double scale, int64_t partition_tokens,
+                              const std::string& merge) {
+  return decode(query, key_cache, value_cache, block_tables, context_lengths, scale, partition_tokens,
+                merge, RK_PA_VARIANT_MFMA, new_key, new_value);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(rk_pa_gfx950, module) {
@@ -194,6 +235,11 @@ PYBIND11_MODULE(rk_pa_gfx950, module) {
              py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
              py::arg("context_lengths"), py::arg("scale"), py::kw_only(),
              py::arg("partition_tokens") = 512, py::arg("merge") = "auto");
+  module.def("decode_append_mfma", &decode_append_mfma,
+             "append each sequence's new token to the paged caches, then paged decode (one launch)",
+             py::arg("query"), py::arg("new_key"), py::arg("new_value"), py::arg("key_cache"),
+             py::arg("value_cache"), py::arg("block_tables"), py::arg("context_lengths"), py::arg("scale"),
+             py::kw_only(), py::arg("partition_tokens") = 512, py::arg("merge") = "auto");
   module.def("decode_valu", &decode_valu, "paged decode, QK^T on fp32 FMAs", py::arg("query"),
              py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
              py::arg("context_lengths"), py::arg("scale"), py::kw_only(),

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "rk_pa_decode",
     "rk_pa_decode_partitions",
     "rk_pa_decode_reduce",
+    "rk_pa_decode_append",
     "rk_pa_decode_fused",
     "rk_pa_decode_counter_words",
     "rk_pa_decode_workspace_bytes",
@@ -83,6 +84,8 @@ class PagedAttentionLibrary:
             getattr(lib, symbol).restype = ctypes.c_int
         lib.rk_pa_decode_fused.argtypes = decode_args[:8] + [vp, sz] + decode_args[8:]
         lib.rk_pa_decode_fused.restype = ctypes.c_int
+        lib.rk_pa_decode_append.argtypes = [vp, vp, vp] + decode_args[1:8] + [vp, sz] + decode_args[8:]
+        lib.rk_pa_decode_append.restype = ctypes.c_int
         lib.rk_pa_decode_counter_words.argtypes = [i64, i64, i64, ctypes.POINTER(sz)]
         lib.rk_pa_decode_counter_words.restype = ctypes.c_int
         lib.rk_pa_last_error.argtypes = []
@@ -117,13 +120,22 @@ class PagedAttentionLibrary:
                   output: int, workspace: int, workspace_bytes: int, batch: int, query_heads: int, kv_heads: int,
                   head_dim: int, num_blocks: int, block_size: int, max_blocks: int, scale: float, dtype: int,
                   index_dtype: int, partition_tokens: int, variant: int, stream: int, phase: str = "all",
-                  counters: int = 0, counter_words: int = 0) -> tuple[Any, tuple[Any, ...]]:
-        """The C entry point of ``phase`` and its argument tuple."""
+                  counters: int = 0, counter_words: int = 0, new_key: int = 0,
+                  new_value: int = 0) -> tuple[Any, tuple[Any, ...]]:
+        """The C entry point of ``phase`` and its argument tuple; with ``new_key`` / ``new_value``,
+        rk_pa_decode_append in the two-launch (``"all"``) or single-launch (``"fused"``) form."""
 
         head = (query, key_cache, value_cache, block_tables, context_lengths, output, workspace or None,
                 workspace_bytes)
         tail = (batch, query_heads, kv_heads, head_dim, num_blocks, block_size, max_blocks, ctypes.c_float(scale),
                 dtype, index_dtype, partition_tokens, variant, stream or None)
+        if new_key or new_value:
+            if phase not in ("all", "fused"):
+                raise ValueError("append-and-decode runs as phase 'all' or 'fused'")
+            fused = phase == "fused"
+            return self.lib.rk_pa_decode_append, (query, new_key or None, new_value or None, *head[1:],
+                                                  (counters or None) if fused else None,
+                                                  counter_words if fused else 0, *tail)
         if phase == "fused":
             return self.lib.rk_pa_decode_fused, (*head, counters or None, counter_words, *tail)
         return getattr(self.lib, PHASES[phase]), (*head, *tail)
@@ -136,8 +148,9 @@ class PagedAttentionLibrary:
 
     def _tensor_call(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
                      scale: float | None, partition_tokens: int, variant: str, out: Any | None,
-                     workspace: Any | None, stream: Any | None, phase: str,
-                     counters: Any | None) -> tuple[Any, Any, tuple[Any, ...], tuple[Any, ...]]:
+                     workspace: Any | None, stream: Any | None, phase: str, counters: Any | None,
+                     new_key: Any | None = None,
+                     new_value: Any | None = None) -> tuple[Any, Any, tuple[Any, ...], tuple[Any, ...]]:
         """(out, C function, its arguments, tensors those arguments point into)."""
 
         import torch
@@ -168,30 +181,36 @@ class PagedAttentionLibrary:
             partition_tokens=partition_tokens, variant=VARIANTS[variant], stream=stream.cuda_stream, phase=phase,
             counters=counters.data_ptr() if counters is not None else 0,
             counter_words=counters.numel() if counters is not None else 0,
+            new_key=new_key.data_ptr() if new_key is not None else 0,
+            new_value=new_value.data_ptr() if new_value is not None else 0,
         )
-        held = (query, key_cache, value_cache, block_tables, context_lengths, out, workspace, counters)
+        held = (query, key_cache, value_cache, block_tables, context_lengths, out, workspace, counters, new_key,
+                new_value)
         return out, function, args, held
 
     def decode(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
                scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
                out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
-               phase: str = "all", counters: Any | None = None) -> Any:
+               phase: str = "all", counters: Any | None = None, new_key: Any | None = None,
+               new_value: Any | None = None) -> Any:
         """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None).
 
         ``counters`` (phase ``"fused"`` only): an int32 tensor of at least ``counter_words`` zeros,
-        allocated zeroed here if None.
+        allocated zeroed here if None.  ``new_key`` / ``new_value`` ([batch, kv_heads, head_dim]):
+        append-and-decode (rk_pa_decode_append), which also writes them into the caches.
         """
 
         out, function, args, _ = self._tensor_call(query, key_cache, value_cache, block_tables, context_lengths,
                                                    scale, partition_tokens, variant, out, workspace, stream, phase,
-                                                   counters)
+                                                   counters, new_key, new_value)
         self.check(function(*args))
         return out
 
     def prepare(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
                 scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
                 out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
-                phase: str = "all", counters: Any | None = None) -> Any:
+                phase: str = "all", counters: Any | None = None, new_key: Any | None = None,
+                new_value: Any | None = None) -> Any:
         """The launch ``decode`` would make, with every argument converted once.
 
         Returns a zero-argument callable that repeats it (one foreign call per launch, no Python
@@ -201,7 +220,7 @@ class PagedAttentionLibrary:
 
         _, function, args, held = self._tensor_call(query, key_cache, value_cache, block_tables, context_lengths,
                                                     scale, partition_tokens, variant, out, workspace, stream,
-                                                    phase, counters)
+                                                    phase, counters, new_key, new_value)
         return _repeatable(function, args, self.check, held)
 
 

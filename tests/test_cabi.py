@@ -42,6 +42,27 @@ def test_library_exports_every_declared_symbol(lib):
     assert lib.version() == "rk_pa_gfx950 1.0.0 (gfx950, wave64)"
 
 
+def test_append_and_decode_argument_assembly(lib):
+    """rk_pa_decode_append takes the new rows after the query and the counters only in the fused
+    form; the split phases cannot carry an append (no call reaches the device here)."""
+
+    shape = dict(query=0x1000, key_cache=0x2000, value_cache=0x3000, block_tables=0x4000, context_lengths=0x5000,
+                 output=0x6000, workspace=0x7000, workspace_bytes=256, batch=2, query_heads=8, kv_heads=2,
+                 head_dim=128, num_blocks=4, block_size=16, max_blocks=2, scale=0.125, dtype=cabi.RK_DTYPE_BF16,
+                 index_dtype=cabi.RK_INDEX_INT32, partition_tokens=16, variant=cabi.VARIANTS["mfma"], stream=0,
+                 counters=0x8000, counter_words=4, new_key=0x9000, new_value=0xA000)
+    function, args = lib._raw_call(**shape, phase="all")
+    assert function == lib.lib.rk_pa_decode_append
+    assert args[:4] == (0x1000, 0x9000, 0xA000, 0x2000) and args[10:12] == (None, 0)
+    function, args = lib._raw_call(**shape, phase="fused")
+    assert function == lib.lib.rk_pa_decode_append and args[10:12] == (0x8000, 4)
+    for phase in ("partitions", "reduce"):
+        with pytest.raises(ValueError):
+            lib._raw_call(**shape, phase=phase)
+    function, _ = lib._raw_call(**{**shape, "new_key": 0, "new_value": 0}, phase="all")
+    assert function == lib.lib.rk_pa_decode
+
+
 def test_status_codes_match_header():
     text = HEADER.read_text()
     for name in ("RK_OK", "RK_ERR_INVALID_ARGUMENT", "RK_ERR_UNSUPPORTED", "RK_ERR_WORKSPACE", "RK_ERR_LAUNCH",

@@ -130,6 +130,19 @@ def test_invalid_new_token_block_is_skipped_and_masked(gpu, palib, kvlib, index_
     check_against_two_operators(palib, kvlib, to_device(case, gpu), 64, "all")
 
 
+@pytest.mark.parametrize("phase", ["all", "fused"])
+def test_context_past_the_table_appends_at_its_last_position(gpu, palib, kvlib, phase):
+    """A context length above max_blocks * block_size is clamped first, as the decode clamps it: the
+    new token takes the table's last position."""
+
+    import torch
+
+    case = make_case(torch, batch=3, query_heads=16, kv_heads=4, head_dim=64, block_size=16, contexts=[40, 200, 64],
+                     max_blocks=4, dtype="fp16", seed=21)
+    announce(f"append-decode context past the table {phase}")
+    check_against_two_operators(palib, kvlib, to_device(case, gpu), 32, phase)
+
+
 def test_valu_variant_is_refused(gpu, palib):
     import torch
 

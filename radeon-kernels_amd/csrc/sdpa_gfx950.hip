@@ -41,6 +41,7 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <numeric>
 #include <string>
 #include <utility>
 
@@ -112,7 +113,8 @@ struct Params {
   const uint16_t* __restrict__ v;  // [B, Hkv, S, D]
   uint16_t* __restrict__ out;      // [B, Hq, S, D]
   int32_t batch, query_heads, kv_heads, group, seq, q_blocks;
-  int32_t xcd_grouped;  // 1: one-dimensional grid in which every XCD owns whole KV groups
+  int32_t xcd_slices;   // 0: two-dimensional grid; else 1-D grid, every XCD owning whole group slices
+  int32_t slice_items;  // workgroups of one group slice: group * ceil(q_blocks / xcd_slices)
   float scale_log2e;
 };
 
@@ -274,25 +276,30 @@ __global__ __launch_bounds__(kThreads, (Tiling<D, BLOCK_N>::kOccupancy)) void sd
   const int col = lane & 31;
 
   // Grid -> (sequence, query head, query block).
-  //   xcd_grouped (grids of several rounds whose KV groups, sequence x KV head, divide into 8): the
-  //     dispatcher places hardware workgroup h on XCD h % 8, so XCD x takes KV groups x, x + 8, ...,
-  //     one after the other, and within a group the query blocks in order (causal: longest first,
-  //     the key range grows with the query block), the group's query heads adjacent.  The
-  //     workgroups resident on one XCD then read one or two groups' K/V (2 MB each at S = 4096,
-  //     D = 128) out of its 4 MB L2.  In the two-dimensional orders below every XCD holds blocks of
-  //     all groups at once and re-streams K/V past its L2: 2.9 GB of L2 fetches per call on the
-  //     4-sequence, 32x8-head, S = 4096 causal case, for 201 MB of Q, K and V.
+  //   xcd_slices = S > 0 (grids of several rounds): a KV group (sequence x KV head) is cut into S
+  //     slices by query-block residue (S = 8 / gcd(groups, 8), 1 when the groups divide into 8), so
+  //     the slices divide into 8.  The dispatcher places hardware workgroup h on XCD h % 8, so XCD x
+  //     takes slices x, x + 8, ... one after the other; within a slice the query blocks go in order
+  //     (causal: longest first, the key range grows with the query block), the group's query heads
+  //     adjacent.  The workgroups resident on one XCD then read one or two groups' K/V (2 MB each at
+  //     S = 4096, D = 128) out of its 4 MB L2.  In the two-dimensional orders below every XCD holds
+  //     blocks of all groups at once and re-streams K/V past its L2: 2.9 GB of L2 fetches per call
+  //     on the 4-sequence, 32x8-head, S = 4096 causal case, for 201 MB of Q, K and V.  Slices hold
+  //     ceil(q_blocks / S) blocks; the padding workgroups of shorter slices exit at once.
   //   Otherwise, causal: x = (sequence, head), y = query block, longest first; noncausal:
   //     x = query block, y = (sequence, head).
   int bh, qb;
-  if (p.xcd_grouped) {
+  if (p.xcd_slices > 0) {
     const int hw = static_cast<int>(blockIdx.x);
-    const int per_group = p.group * p.q_blocks;  // workgroups of one KV group
-    const int local = (hw >> 3) / per_group;     // the XCD's local-th group
-    const int r = (hw >> 3) - local * per_group;
-    const int kv_group = local * 8 + (hw & 7);   // b * Hkv + hkv
+    const int local = (hw >> 3) / p.slice_items;   // the XCD's local-th slice
+    const int r = (hw >> 3) - local * p.slice_items;
+    const int vslice = local * 8 + (hw & 7);
+    const int kv_group = vslice / p.xcd_slices;    // b * Hkv + hkv
+    const int residue = vslice - kv_group * p.xcd_slices;
     const int rank = r / p.group;
-    qb = CAUSAL ? p.q_blocks - 1 - rank : rank;
+    const int ordinal = rank * p.xcd_slices + residue;  // position in the group's block order
+    if (ordinal >= p.q_blocks) return;                   // padding
+    qb = CAUSAL ? p.q_blocks - 1 - ordinal : ordinal;
     const int seq_index = kv_group / p.kv_heads;
     bh = seq_index * p.query_heads + (kv_group - seq_index * p.kv_heads) * p.group + (r - rank * p.group);
   } else {
@@ -596,11 +603,18 @@ extern "C" int rk_sdpa_forward(const void* query, const void* key, const void* v
   prm.seq = static_cast<int32_t>(sequence);
   prm.q_blocks = static_cast<int32_t>(q_blocks);
   prm.scale_log2e = scale * kLog2e;
-  // XCD-owned KV groups need whole groups per XCD (a remainder would leave XCDs idle); grids of one
-  // round are resident at once, and keep the two-dimensional orders they were tuned with.
+  // Grids of one round are resident at once and keep the two-dimensional orders they were tuned
+  // with; larger grids take XCD-owned group slices (the one-dimensional grid holds every slice's
+  // ceil(q_blocks / S) blocks, padding included, and stays a multiple of 8).
   const int64_t workgroups = batch * query_heads * q_blocks;
-  prm.xcd_grouped = (batch * kv_heads) % 8 == 0 && workgroups > kWideGrid ? 1 : 0;
-  const dim3 grid = prm.xcd_grouped ? dim3(static_cast<uint32_t>(workgroups))
+  const int64_t groups = batch * kv_heads;
+  const int64_t slices = 8 / std::gcd(groups, int64_t{8});
+  const int64_t slice_items = (query_heads / kv_heads) * ((q_blocks + slices - 1) / slices);
+  const int64_t grid_1d = groups * slices * slice_items;
+  const bool sliced = workgroups > kWideGrid && grid_1d < (int64_t{1} << 31);
+  prm.xcd_slices = sliced ? static_cast<int32_t>(slices) : 0;
+  prm.slice_items = static_cast<int32_t>(slice_items);
+  const dim3 grid = sliced ? dim3(static_cast<uint32_t>(grid_1d))
                     : is_causal ? dim3(static_cast<uint32_t>(batch * query_heads), static_cast<uint32_t>(q_blocks))
                                 : dim3(static_cast<uint32_t>(q_blocks), static_cast<uint32_t>(batch * query_heads));
   hipStream_t hs = static_cast<hipStream_t>(stream);

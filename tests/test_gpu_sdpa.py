@@ -103,12 +103,14 @@ def test_shapes_and_tails(gpu, sdpalib, shape, dtype):
 
 # Grids of more than 768 workgroups (three rounds' worth on 256 CUs) run head_dim 128 in its 32-key
 # form; the shapes above all launch fewer.  B, Hq, Hkv, S, D, causal; workgroups = B * Hq * ceil(S / 128).
-# Sequence x KV head counts that divide into 8 take the XCD-owned grid order, the others the
-# two-dimensional ones.
+# They take the XCD-owned grid order: each KV group cut into 8 / gcd(groups, 8) slices of query blocks
+# (with padding workgroups when the slices are uneven).
 WIDE = [
-    (4, 32, 8, 1024, 128, True),   # 1024 workgroups, 32 KV groups (XCD-owned)
-    (5, 64, 8, 300, 128, False),   # 960, ragged tail block, 40 KV groups (XCD-owned)
-    (3, 96, 12, 333, 128, True),   # 864, ragged, group of 8, 36 KV groups (two-dimensional)
+    (4, 32, 8, 1024, 128, True),   # 1024 workgroups, 32 KV groups (1 slice each)
+    (5, 64, 8, 300, 128, False),   # 960, ragged tail block, 40 KV groups
+    (3, 96, 12, 333, 128, True),   # 864, ragged, group of 8, 36 KV groups (2 slices, padding)
+    (1, 64, 4, 1700, 64, True),    # 896, 4 KV groups (2 slices), group of 16
+    (3, 24, 3, 1300, 128, False),  # 792, 9 KV groups (8 slices, padding)
     (2, 32, 8, 1700, 64, True),    # 896, ragged, head_dim 64, 16 KV groups (XCD-owned)
     (2, 16, 4, 3100, 256, False),  # 800, ragged, head_dim 256, 8 KV groups (XCD-owned)
     (32, 32, 8, 70, 128, True),    # 1024, one ragged query block per head, 256 KV groups (XCD-owned)

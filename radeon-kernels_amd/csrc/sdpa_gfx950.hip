@@ -126,10 +126,10 @@ constexpr int kWaitLgkmcnt0 = 0xC07F;
 // Keys per block BN and workgroups per CU.  head_dim 256 takes 32-key blocks (its four tiles then stay
 // within the 64 KB the ds offset field addresses) at one workgroup per CU, whose 512 registers per
 // lane hold its accumulators without spilling (two per CU spilled and ran 5-9% slower).  head_dim
-// 128 has two forms: 64-key blocks at two workgroups per
-// CU (fewer barriers: faster when the grid is at most one round of workgroups) and 32-key blocks at
-// three (more waves to overlap one another's softmax and MFMAs, and a finer causal diagonal: faster
-// on grids of several rounds).
+// 64 and 128 take 64-key blocks at two workgroups per CU (fewer barriers per key).  A 32-key form of
+// head_dim 128 at three workgroups per CU was faster on grids of several rounds only while those
+// grids re-streamed K/V past L2; with the XCD-owned grid order the 64-key form is 0.3-3% faster
+// there too, so it is the only one built.
 template <int D, int BN>
 struct Tiling {
   static_assert(BN == 32 || BN == 64, "32 or 64 keys per block");
@@ -539,7 +539,7 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-// head_dim 128 grids above one round of three workgroups on each of the 256 CUs take the 32-key form.
+// Grids above one round of three workgroups on each of the 256 CUs take the XCD-owned grid order.
 constexpr int64_t kWideGrid = 3 * 256;
 
 template <class E, int D, int BN>
@@ -552,11 +552,8 @@ void launch_d(const Params& prm, bool causal, dim3 grid, hipStream_t stream) {
 
 template <class E>
 void launch_e(const Params& prm, int64_t head_dim, bool causal, dim3 grid, hipStream_t stream) {
-  const int64_t workgroups = static_cast<int64_t>(grid.x) * grid.y;
   if (head_dim == 64)
     launch_d<E, 64, 64>(prm, causal, grid, stream);
-  else if (head_dim == 128 && workgroups > kWideGrid)
-    launch_d<E, 128, 32>(prm, causal, grid, stream);
   else if (head_dim == 128)
     launch_d<E, 128, 64>(prm, causal, grid, stream);
   else

@@ -101,8 +101,8 @@ def test_shapes_and_tails(gpu, sdpalib, shape, dtype):
     check(out.cpu(), q, k, v, causal, dtype, what=f"{shape}/{dtype}")
 
 
-# Grids of more than 768 workgroups (three rounds' worth on 256 CUs) run head_dim 128 in its 32-key
-# form; the shapes above all launch fewer.  B, Hq, Hkv, S, D, causal; workgroups = B * Hq * ceil(S / 128).
+# Grids of more than 768 workgroups (three rounds' worth on 256 CUs) take the XCD-owned grid order;
+# the shapes above all launch fewer.  B, Hq, Hkv, S, D, causal; workgroups = B * Hq * ceil(S / 128).
 # They take the XCD-owned grid order: each KV group cut into 8 / gcd(groups, 8) slices of query blocks
 # (with padding workgroups when the slices are uneven).
 WIDE = [

@@ -53,7 +53,6 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kBlockM = 128;  // queries per workgroup (32 per wave)
-constexpr int kBlockN = 64;   // keys per block
 constexpr float kLog2e = 1.4426950408889634f;
 // How far (log2 units) the softmax reference may trail the running maximum before a rescale.
 constexpr float kRescaleSlack = 8.0f;

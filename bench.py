@@ -244,7 +244,7 @@ def main_sdpa(args) -> int:
     import torch
 
     from radeon_kernels.cabi import sdpa_library
-    from radeon_kernels.workloads import SDPA_CASES, SDPA_LONG_CASES, make_sdpa_inputs
+    from benchmarks.workloads import SDPA_CASES, SDPA_LONG_CASES, make_sdpa_inputs
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no visible ROCm GPU"}))
@@ -365,7 +365,7 @@ def main_kv(args) -> int:
     import torch
 
     from radeon_kernels.cabi import kv_library
-    from radeon_kernels.workloads import APPEND_CASES, COPY_CASES, make_append_inputs, make_copy_inputs
+    from benchmarks.workloads import APPEND_CASES, COPY_CASES, make_append_inputs, make_copy_inputs
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no visible ROCm GPU"}))
@@ -514,7 +514,7 @@ def main(argv=None) -> int:
     import torch
 
     from radeon_kernels.cabi import library
-    from radeon_kernels.workloads import WORKLOADS, make_inputs
+    from benchmarks.workloads import WORKLOADS, make_inputs
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no visible ROCm GPU"}))
@@ -531,7 +531,7 @@ def main(argv=None) -> int:
     if args.calibration_copy:
         calibration_copy(torch, device)
 
-    data = make_inputs(w, device=device, generator_device=device if w.ragged else "cpu")
+    data = make_inputs(w, device=device)
     kv_bytes = data["kv_bytes"]
     cache_bytes = data["key_cache"].numel() * 2 * 2
     # Small workloads fit in the 256 MB last-level cache: rotate among enough K/V copies that each

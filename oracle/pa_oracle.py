@@ -134,11 +134,13 @@ def decode_numpy(
         k = key_cache[phys, offs].astype(accum)  # [ctx, Hkv, D]
         v = value_cache[phys, offs].astype(accum)
         q = query[b].astype(accum).reshape(kv_heads, group, head_dim)  # head h -> kv h // group
-        scores = np.einsum("kgd,tkd->kgt", q, k) * factor
+        # scores[k, g, t] = sum_d q[k, g, d] * k[t, k, d], as one matmul per KV head (BLAS-backed).
+        scores = np.matmul(q, k.transpose(1, 2, 0)) * factor
         peak = scores.max(axis=-1, keepdims=True)
         weights = np.exp(scores - peak)
         weights /= weights.sum(axis=-1, keepdims=True)
-        out[position] = np.einsum("kgt,tkd->kgd", weights, v).reshape(query_heads, head_dim)
+        # out[k, g, d] = sum_t weights[k, g, t] * v[t, k, d]
+        out[position] = np.matmul(weights, v.transpose(1, 0, 2)).reshape(query_heads, head_dim)
     return out
 
 

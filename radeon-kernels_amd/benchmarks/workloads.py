@@ -1,10 +1,19 @@
-"""Seeded paged-decode workloads: the five measured shapes and a generic builder.
+"""Seeded paged-decode workloads: the five measured shapes, the reference's workload cases and a
+generic builder.
 
 Each workload fixes batch, heads, head_dim, block size, dtype, cache size and how block tables and
-context lengths are drawn.  Inputs come from a ``torch.Generator`` seeded per workload, drawn in a
-fixed order (context lengths, block permutation, query, keys, values) so that a seed names one
-input set.  Generation on the CPU is bit-reproducible on every machine; generation on a GPU is
-reproducible for a given torch build and is used for the 4.5 GB ragged workload.
+context lengths are drawn.  Inputs are drawn on the CPU, so a seed names one input set on every
+machine, in a fixed order: context lengths, block permutation, query, keys, values.
+
+* ``draw="serial"``: every tensor from one ``torch.Generator`` seeded with the workload seed.
+* ``draw="chunked"`` (the 4.8 GB ragged workload): context lengths, permutation and query as above;
+  each cache is drawn in fixed chunks of ``CHUNK_ELEMENTS`` values, chunk ``i`` of cache ``c``
+  (0 = keys, 1 = values) from its own generator seeded ``chunk_seed(seed, c, i)``.  The chunks are
+  independent, so they are drawn on a thread pool; the result does not depend on the number of
+  threads.
+
+``input_digests`` gives the SHA-256 of every input tensor's bytes, which ties a test's inputs to a
+benchmark run's.
 
 KV accounting (``kv_bytes``) counts the K and V rows a decode must read: for every sequence,
 ``min(context, max_blocks * block_size)`` tokens x kv_heads x head_dim x 2 tensors x element size.
@@ -13,11 +22,15 @@ Padding table entries and tokens past the context are not counted.
 
 from __future__ import annotations
 
+import hashlib
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from typing import Any
 
 DEFAULT_SEED_BASE = 20261201
+CHUNK_ELEMENTS = 1 << 24
 
 
 @dataclass(frozen=True)
@@ -36,6 +49,10 @@ class Workload:
     kv_std: float = 1.0
     seed: int = DEFAULT_SEED_BASE
     notes: str = ""
+    # "normal": q ~ N(0, 1), K/V ~ N(0, kv_std^2).  "uniform": q, K, V ~ U(-0.125, 0.125), the
+    # reference benchmark's draw (benchmarks/paged_attention/benchmark.py:74-77).
+    distribution: str = "normal"
+    draw: str = "serial"  # "serial" | "chunked" (see the module docstring)
     extra: dict[str, Any] = field(default_factory=dict)
 
     @property
@@ -71,14 +88,78 @@ WORKLOADS: dict[str, Workload] = {
     "c5": Workload(
         key="c5", name="b128-gqa32x8-ragged1024to16384-d128-p16-bf16", batch=128, query_heads=32, kv_heads=8,
         head_dim=128, block_size=16, dtype="bf16", max_blocks=1024, num_blocks=None, context=(1024, 16384),
-        seed=DEFAULT_SEED_BASE + 4,
+        seed=DEFAULT_SEED_BASE + 4, draw="chunked",
         notes="context ~ U[1024, 16384]; tables padded to 1024 with block 0; blocks assigned by seeded shuffle",
     ),
 }
 
+# The reference's paged-decode workload cases (benchmarks/workloads/paged_attention_decode-1.0.yaml:13-22),
+# each in fp16 and bf16, drawn as the reference's benchmark draws them (benchmark.py:79-117): every
+# sequence has the case's context length, num_blocks = batch * ceil(context / block_size), the tables
+# are one permutation of all blocks, and q, K, V ~ U(-0.125, 0.125).  Seeds are the benchmark's three
+# (benchmark.py:200), used with a CPU generator.
+REFERENCE_CASES: tuple[tuple[str, int, int, int, int, int, int], ...] = (
+    # id, batch, query_heads, kv_heads, context, head_dim, block_size
+    ("b1-gqa32x8-c128-d128-p16", 1, 32, 8, 128, 128, 16),
+    ("b1-gqa32x8-c1024-d128-p16", 1, 32, 8, 1024, 128, 16),
+    ("b1-gqa32x8-c4096-d128-p16", 1, 32, 8, 4096, 128, 16),
+    ("b8-gqa32x8-c128-d128-p16", 8, 32, 8, 128, 128, 16),
+    ("b8-gqa32x8-c1024-d128-p16", 8, 32, 8, 1024, 128, 16),
+    ("b16-gqa32x8-c2048-d128-p16", 16, 32, 8, 2048, 128, 16),
+    ("b4-mha16-c2048-d64-p32", 4, 16, 16, 2048, 64, 32),
+    ("b4-gqa32x8-c1024-d256-p16", 4, 32, 8, 1024, 256, 16),
+)
+REFERENCE_SEEDS = (20260918, 20260919, 20260920)
+
+
+def _reference_workload(case: tuple[str, int, int, int, int, int, int], dtype: str) -> Workload:
+    case_id, batch, hq, hkv, context, head_dim, block_size = case
+    max_blocks = math.ceil(context / block_size)
+    return Workload(
+        key=f"{case_id}-{dtype}", name=f"{case_id}-{dtype}", batch=batch, query_heads=hq, kv_heads=hkv,
+        head_dim=head_dim, block_size=block_size, dtype=dtype, max_blocks=max_blocks,
+        num_blocks=batch * max_blocks, context=context, seed=REFERENCE_SEEDS[0], distribution="uniform",
+        notes="reference workload case: one permutation of batch * max_blocks blocks, q/K/V ~ U(-0.125, 0.125)",
+    )
+
+
+for _case in REFERENCE_CASES:
+    for _dtype in ("fp16", "bf16"):
+        _w = _reference_workload(_case, _dtype)
+        WORKLOADS[_w.key] = _w
+REFERENCE_KEYS = tuple(f"{case[0]}-{dtype}" for case in REFERENCE_CASES for dtype in ("fp16", "bf16"))
+
 
 def torch_dtype(torch: Any, name: str) -> Any:
     return {"fp16": torch.float16, "bf16": torch.bfloat16}[name]
+
+
+def chunk_seed(seed: int, cache: int, chunk: int) -> int:
+    """Seed of chunk ``chunk`` of cache ``cache`` (0 keys, 1 values) in the chunked draw."""
+
+    return (seed << 24) + (cache << 20) + chunk
+
+
+def _chunked_normal(torch: Any, shape: tuple[int, ...], std: float, dtype: Any, seed: int, cache: int,
+                    workers: int | None) -> Any:
+    out = torch.empty(shape, dtype=dtype)
+    flat = out.view(-1)
+    total = flat.numel()
+
+    def fill(chunk: int) -> None:
+        start = chunk * CHUNK_ELEMENTS
+        count = min(CHUNK_ELEMENTS, total - start)
+        gen = torch.Generator().manual_seed(chunk_seed(seed, cache, chunk))
+        values = torch.randn(count, generator=gen, dtype=torch.float32)
+        if std != 1.0:
+            values.mul_(std)
+        flat[start:start + count].copy_(values)
+
+    chunks = (total + CHUNK_ELEMENTS - 1) // CHUNK_ELEMENTS
+    workers = workers or min(16, os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        list(pool.map(fill, range(chunks)))
+    return out
 
 
 def make_inputs(
@@ -86,32 +167,31 @@ def make_inputs(
     *,
     seed: int | None = None,
     device: Any = "cpu",
-    generator_device: Any | None = None,
     index_dtype: str = "int32",
     torch_module: Any | None = None,
+    workers: int | None = None,
 ) -> dict[str, Any]:
-    """Draw the workload's tensors; returns query, key_cache, value_cache, block_tables,
-    context_lengths (all on ``device``) plus ``num_blocks`` and ``kv_bytes``."""
+    """Draw the workload's tensors on the CPU; returns query, key_cache, value_cache, block_tables,
+    context_lengths (all on ``device``) plus ``num_blocks``, ``kv_bytes`` and ``contexts``."""
 
     if torch_module is None:
         import torch as torch_module
     torch = torch_module
     w = WORKLOADS[workload] if isinstance(workload, str) else workload
     seed = w.seed if seed is None else seed
-    gen_device = torch.device(generator_device if generator_device is not None else "cpu")
-    generator = torch.Generator(device=gen_device).manual_seed(seed)
+    generator = torch.Generator().manual_seed(seed)
     index = {"int32": torch.int32, "int64": torch.int64}[index_dtype]
     dtype = torch_dtype(torch, w.dtype)
 
     if w.ragged:
         low, high = w.context
-        contexts = torch.randint(low, high + 1, (w.batch,), generator=generator, device=gen_device).cpu()
+        contexts = torch.randint(low, high + 1, (w.batch,), generator=generator)
     else:
         contexts = torch.full((w.batch,), int(w.context), dtype=torch.int64)
     needed = [math.ceil(int(c) / w.block_size) for c in contexts]
     if w.num_blocks is None:
         num_blocks = int(sum(needed))
-        permutation = torch.randperm(num_blocks, generator=generator, device=gen_device).cpu()
+        permutation = torch.randperm(num_blocks, generator=generator)
         tables = torch.zeros((w.batch, w.max_blocks), dtype=torch.int64)
         cursor = 0
         for b, count in enumerate(needed):
@@ -119,19 +199,29 @@ def make_inputs(
             cursor += count
     else:
         num_blocks = w.num_blocks
-        permutation = torch.randperm(num_blocks, generator=generator, device=gen_device).cpu()
+        permutation = torch.randperm(num_blocks, generator=generator)
         tables = permutation[: w.batch * w.max_blocks].view(w.batch, w.max_blocks).clone()
 
-    def normal(shape: tuple[int, ...], std: float) -> Any:
-        values = torch.randn(shape, generator=generator, device=gen_device, dtype=torch.float32)
-        if std != 1.0:
-            values.mul_(std)
+    def draw(shape: tuple[int, ...], std: float) -> Any:
+        if w.distribution == "uniform":
+            values = torch.rand(shape, generator=generator, dtype=torch.float32).mul_(0.25).sub_(0.125)
+        else:
+            values = torch.randn(shape, generator=generator, dtype=torch.float32)
+            if std != 1.0:
+                values.mul_(std)
         return values.to(dtype=dtype)
 
     cache_shape = (num_blocks, w.block_size, w.kv_heads, w.head_dim)
-    query = normal((w.batch, w.query_heads, w.head_dim), 1.0)
-    key_cache = normal(cache_shape, w.kv_std)
-    value_cache = normal(cache_shape, w.kv_std)
+    query = draw((w.batch, w.query_heads, w.head_dim), 1.0)
+    if w.draw == "chunked":
+        if w.distribution != "normal":
+            raise ValueError("the chunked draw is defined for normal values only")
+        key_cache = _chunked_normal(torch, cache_shape, w.kv_std, dtype, seed, 0, workers)
+        value_cache = _chunked_normal(torch, cache_shape, w.kv_std, dtype, seed, 1, workers)
+    else:
+        key_cache = draw(cache_shape, w.kv_std)
+        value_cache = draw(cache_shape, w.kv_std)
+    context_list = [int(c) for c in contexts]
     return {
         "query": query.to(device),
         "key_cache": key_cache.to(device),
@@ -139,10 +229,26 @@ def make_inputs(
         "block_tables": tables.to(dtype=index).to(device),
         "context_lengths": contexts.to(dtype=index).to(device),
         "num_blocks": num_blocks,
-        "kv_bytes": kv_bytes(w, [int(c) for c in contexts]),
+        "kv_bytes": kv_bytes(w, context_list),
+        "contexts": context_list,
         "workload": w,
         "seed": seed,
     }
+
+
+INPUT_NAMES = ("query", "key_cache", "value_cache", "block_tables", "context_lengths")
+
+
+def input_digests(data: dict[str, Any], workers: int = 5) -> dict[str, str]:
+    """SHA-256 of the bytes of every input tensor (copied to the host), keyed by input name."""
+
+    def digest(name: str) -> tuple[str, str]:
+        tensor = data[name].detach().contiguous().cpu()
+        raw = tensor.view(-1).view(__import__("torch").uint8).numpy()
+        return name, hashlib.sha256(memoryview(raw)).hexdigest()
+
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        return dict(pool.map(digest, INPUT_NAMES))
 
 
 def kv_bytes(workload: Workload, contexts: list[int]) -> int:

@@ -55,7 +55,7 @@ HEADLINE = {
     "kv_cache_copy": "beam-pairs32-mha32-d128-p32",
     "sdpa": "b1-gqa32x8-s512-d128-causal",
 }
-# Exact paged-attention dispatch regions -> workload keys of radeon_kernels.workloads.
+# Exact paged-attention dispatch regions -> workload keys of benchmarks.workloads.
 PA_WORKLOADS = {
     "b1-gqa32x8-c128-d128-p16-fp16": "c1",
     "b8-gqa32x8-c1024-d128-p16-bf16": "c2",
@@ -148,7 +148,7 @@ def time_pair(torch, candidate, baseline, *, samples: int) -> dict:
 def evaluate_paged_attention(torch, samples: int) -> dict:
     import radeon_kernels as rk
     from radeon_kernels.ops.paged_attention.reference import paged_attention_decode_reference as fallback
-    from radeon_kernels.workloads import WORKLOADS, make_inputs
+    from benchmarks.workloads import WORKLOADS, make_inputs
 
     device = torch.device("cuda:0")
 
@@ -166,7 +166,7 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
     for suffix, key in PA_WORKLOADS.items():
         w = WORKLOADS[key]
         for seed in range(w.seed, w.seed + SEEDS_PER_CASE):
-            data = make_inputs(w, seed=seed, device=device, generator_device=device if w.ragged else "cpu")
+            data = make_inputs(w, seed=seed, device=device)
             args = (data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
                     data["context_lengths"])
             sys.stderr.write(f"[case] paged_attention_decode {suffix} seed {seed}\n")
@@ -185,7 +185,7 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
             torch.cuda.empty_cache()
 
     w = WORKLOADS[PA_WORKLOADS[HEADLINE["paged_attention_decode"]]]
-    data = make_inputs(w, device=device, generator_device=device)
+    data = make_inputs(w, device=device)
     args = (data["query"], data["key_cache"], data["value_cache"], data["block_tables"], data["context_lengths"])
     chunk = 8
 
@@ -209,7 +209,7 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
 def evaluate_sdpa(torch, samples: int) -> dict:
     import radeon_kernels as rk
     from radeon_kernels.ops.sdpa.reference import sdpa_fallback, sdpa_reference
-    from radeon_kernels.workloads import SDPA_CASES, SDPA_SEED, make_sdpa_inputs
+    from benchmarks.workloads import SDPA_CASES, SDPA_SEED, make_sdpa_inputs
 
     device = torch.device("cuda:0")
     cases = []
@@ -250,7 +250,7 @@ def evaluate_sdpa(torch, samples: int) -> dict:
 def evaluate_kv(torch, operator: str, samples: int) -> dict:
     import radeon_kernels as rk
     from radeon_kernels.ops.kv_cache.reference import kv_cache_append_reference, kv_cache_copy_reference
-    from radeon_kernels.workloads import (APPEND_CASES, APPEND_SEED, COPY_CASES, COPY_SEED, make_append_inputs,
+    from benchmarks.workloads import (APPEND_CASES, APPEND_SEED, COPY_CASES, COPY_SEED, make_append_inputs,
                                           make_copy_inputs)
 
     device = torch.device("cuda:0")

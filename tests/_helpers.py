@@ -91,6 +91,39 @@ def oracle64(case: dict[str, Any], scale: float | None = None, sequences=None) -
     )
 
 
+def oracle64_rows(case: dict[str, Any], scale: float | None = None, workers: int = 8) -> np.ndarray:
+    """float64 oracle of every sequence of a large CPU-resident case, one sequence at a time.
+
+    Each sequence's blocks are gathered first (``index_select`` of its table entries up to its
+    context), so only the rows it attends to are converted to float; the sequences run on a thread
+    pool (numpy's matrix products release the GIL).
+    """
+
+    import math as _math
+    from concurrent.futures import ThreadPoolExecutor
+
+    import torch
+
+    query, key_cache, value_cache = case["query"], case["key_cache"], case["value_cache"]
+    tables, contexts = case["block_tables"].cpu(), case["context_lengths"].cpu()
+    block_size = int(key_cache.shape[1])
+    cap = int(tables.shape[1]) * block_size
+    f = pa_oracle.as_numpy_f32
+
+    def one(b: int) -> np.ndarray:
+        ctx = min(int(contexts[b]), cap)
+        blocks = max(1, _math.ceil(max(ctx, 0) / block_size))
+        ids = tables[b, :blocks].to(torch.int64)
+        compact = np.arange(blocks, dtype=np.int64)[None]
+        return pa_oracle.decode_numpy(f(query[b:b + 1]), f(key_cache.index_select(0, ids)),
+                                      f(value_cache.index_select(0, ids)), compact, [ctx], scale,
+                                      accum=np.float64)[0]
+
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        rows = list(pool.map(one, range(int(query.shape[0]))))
+    return np.stack(rows)
+
+
 def max_abs_error(actual: Any, expected: np.ndarray) -> float:
     got = pa_oracle.as_numpy_f32(actual).astype(np.float64)
     if got.shape != expected.shape:

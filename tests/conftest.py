@@ -45,3 +45,23 @@ def kvlib(gpu):
     from radeon_kernels.cabi import kv_library
 
     return kv_library()
+
+
+@pytest.fixture(scope="session")
+def c5_case(gpu):
+    """The 128-sequence ragged workload drawn on the CPU (checked against its committed SHA-256
+    digests), its float64 oracle over all 128 sequences, and a GPU copy of its inputs."""
+
+    import json
+
+    from _helpers import oracle64_rows, to_device
+    from benchmarks.workloads import input_digests, make_inputs
+
+    golden = json.loads((ROOT / "tests" / "golden" / "c5_inputs.json").read_text())
+    data = make_inputs("c5")
+    assert data["contexts"] == golden["contexts"] and data["num_blocks"] == golden["num_blocks"]
+    assert input_digests(data) == golden["sha256"], "c5 inputs differ from the committed digests"
+    sys.stderr.write("[case] c5 oracle over 128 sequences\n")
+    sys.stderr.flush()
+    expected = oracle64_rows(data)
+    return {"cpu": data, "gpu": to_device(data, gpu), "expected": expected}

@@ -1,6 +1,7 @@
 """Regenerate the committed paged-attention fixtures in this directory.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py            # everything
+    python tests/golden/make_golden.py c5         # only c5_inputs.json
 
 Writes:
   tiny_cases.npz   small decode cases (inputs as raw 16-bit patterns, float64 expected outputs from
@@ -11,6 +12,9 @@ Writes:
                    boundaries 1, block_size, block_size+1.
   c1_expected.npz  the 1-sequence 32/8-head d128 fp16 workload: SHA-256 of each seeded input
                    tensor, float64 brute-force output and its fp16 rounding.
+  c5_inputs.json   the 128-sequence ragged workload's context lengths, block count, KV bytes and the
+                   SHA-256 of each seeded input tensor (its caches are 2 x 2.1 GB, so only their
+                   digests are kept; the GPU tests and the benchmark recompute and compare them).
   reference_dispatch_{paged_attention_decode,kv_cache_append,kv_cache_copy,sdpa}-1.0.json
                    the reference's published dispatch manifests for these operators (data,
                    Apache-2.0), used to prove the gfx950 entries merge into them; copied from
@@ -80,9 +84,22 @@ def brute(query, key, value, tables, contexts) -> np.ndarray:
                                                   tables.tolist(), contexts.tolist()), dtype=np.float64)
 
 
+def write_c5_digests() -> None:
+    from benchmarks.workloads import input_digests, make_inputs
+
+    data = make_inputs("c5")
+    record = {"workload": data["workload"].name, "seed": data["seed"], "num_blocks": data["num_blocks"],
+              "kv_bytes": data["kv_bytes"], "contexts": data["contexts"], "sha256": input_digests(data)}
+    (HERE / "c5_inputs.json").write_text(json.dumps(record, indent=1, sort_keys=True) + "\n", encoding="utf-8")
+
+
 def main() -> None:
     import torch
 
+    if sys.argv[1:] == ["c5"]:
+        write_c5_digests()
+        return
+    write_c5_digests()
     arrays: dict[str, np.ndarray] = {}
     for name, b, hq, hkv, d, bs, tables, contexts, dtype, seed in TINY_CASES:
         q, k, v, bt, cl = tiny_case_inputs(torch, b, hq, hkv, d, bs, tables, contexts, dtype, seed)
@@ -97,7 +114,7 @@ def main() -> None:
         arrays[f"{name}/expected_rounded"] = pa_oracle.round_to(expected.astype(np.float32), dtype)
     np.savez_compressed(HERE / "tiny_cases.npz", **arrays)
 
-    from radeon_kernels.workloads import make_inputs
+    from benchmarks.workloads import make_inputs
 
     data = make_inputs("c1")
     expected = brute(data["query"], data["key_cache"], data["value_cache"], data["block_tables"],

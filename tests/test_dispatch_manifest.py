@@ -25,7 +25,7 @@ from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint
 from radeon_kernels.runtime.pack import KernelPack
 from radeon_kernels.runtime.registry import DispatchManifest, DispatchRegistry
 from radeon_kernels.runtime.resources import builtin_contract, builtin_dispatch_registry
-from radeon_kernels.workloads import WORKLOADS
+from benchmarks.workloads import WORKLOADS
 from test_api import CaptureRuntime, FakeTensor, FakeTorch
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -204,7 +204,7 @@ def kv_select(signature):
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("index", ["int32", "int64"])
 def test_kv_append_cases_select_their_exact_entry(key, dtype, index):
-    from radeon_kernels.workloads import APPEND_CASES
+    from benchmarks.workloads import APPEND_CASES
 
     decision = kv_select(kv_signature(APPEND_CASES[key], dtype, index))
     assert decision.entry_id == f"kv_cache_append-gfx950-{key}"
@@ -213,7 +213,7 @@ def test_kv_append_cases_select_their_exact_entry(key, dtype, index):
 
 
 def test_kv_append_other_shapes_use_broad_region_or_fall_back():
-    from radeon_kernels.workloads import AppendCase
+    from benchmarks.workloads import AppendCase
 
     broad = kv_select(kv_signature(AppendCase("x", 77, 999, 8, 4, 64)))
     assert broad.entry_id == "kv_cache_append-gfx950-region"
@@ -270,7 +270,7 @@ def copy_signature(case, dtype="bf16", index="int64"):
 @pytest.mark.parametrize("key", sorted(k for k, _ in dispatch_plan.KV_COPY_EXACT_REGIONS))
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_kv_copy_cases_select_their_exact_entry(key, dtype):
-    from radeon_kernels.workloads import COPY_CASES
+    from benchmarks.workloads import COPY_CASES
 
     decision = Dispatcher(builtin_dispatch_registry()).select(
         DispatchRequest("kv_cache_copy", "1.0", copy_signature(COPY_CASES[key], dtype)), gfx950_fingerprint())

@@ -64,7 +64,7 @@ def check_against_two_operators(palib, kvlib, dev, partition, phase, seed=5, var
 @pytest.mark.parametrize("phase", ["all", "fused"])
 @pytest.mark.parametrize("key", ["c1", "c2", "c3", "c4"])
 def test_measured_workloads(gpu, palib, kvlib, key, phase):
-    from radeon_kernels.workloads import make_inputs
+    from benchmarks.workloads import make_inputs
 
     dev = make_inputs(key, device=gpu)
     announce(f"append-decode {key} P={WORKLOAD_PARTITIONS[key]} {phase}")
@@ -75,10 +75,10 @@ def test_measured_workloads(gpu, palib, kvlib, key, phase):
 def test_ragged_b128_workload(gpu, palib, kvlib, phase):
     import torch
 
-    from radeon_kernels.workloads import make_inputs
+    from benchmarks.workloads import make_inputs
 
     announce(f"append-decode c5 ragged b128 {phase}")
-    dev = make_inputs("c5", device=gpu, generator_device=gpu)
+    dev = make_inputs("c5", device=gpu)
     check_against_two_operators(palib, kvlib, dev, WORKLOAD_PARTITIONS["c5"], phase)
     del dev
     torch.cuda.empty_cache()
@@ -166,7 +166,7 @@ def test_torch_binding_matches_append_then_decode(gpu, merge):
 
     import radeon_kernels as rk
     from radeon_kernels.cabi import LIBRARY_PATH
-    from radeon_kernels.workloads import make_inputs
+    from benchmarks.workloads import make_inputs
 
     path = LIBRARY_PATH.parent / "rk_pa_gfx950.so"
     spec = importlib.util.spec_from_file_location("rk_pa_gfx950", path)

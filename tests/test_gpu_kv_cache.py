@@ -19,7 +19,7 @@ import pytest
 
 from _helpers import announce, assert_within, make_case, oracle64, to_device
 from oracle import kv_oracle
-from radeon_kernels.workloads import APPEND_CASES, AppendCase, make_append_inputs
+from benchmarks.workloads import APPEND_CASES, AppendCase, make_append_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -156,7 +156,7 @@ def test_append_then_decode_reads_the_new_tokens(gpu, kvlib, palib):
 
 # ---------------------------------------------------------------------------------------------
 # Block copy (contracts/kv_cache_copy-1.0.json: bit-exact, snapshot semantics)
-from radeon_kernels.workloads import COPY_CASES, CopyCase, make_copy_inputs  # noqa: E402
+from benchmarks.workloads import COPY_CASES, CopyCase, make_copy_inputs  # noqa: E402
 
 
 def expected_copy_bits(data):

@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 def test_decode_prepared_matches_wrapper(gpu, palib, key, partition, phase):
     import torch
 
-    from radeon_kernels.workloads import make_inputs
+    from benchmarks.workloads import make_inputs
 
     data = make_inputs(key, device=gpu)
     q, kc, vc, bt, cl = (data[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths"))
@@ -44,7 +44,7 @@ def test_decode_prepared_matches_wrapper(gpu, palib, key, partition, phase):
 def test_append_prepared_matches_wrapper(gpu, kvlib, case):
     import torch
 
-    from radeon_kernels.workloads import make_append_inputs
+    from benchmarks.workloads import make_append_inputs
 
     data = make_append_inputs(case, dtype="bf16", index_dtype="int64", device=gpu)
     announce(f"prepared append {case}")
@@ -62,7 +62,7 @@ def test_append_prepared_matches_wrapper(gpu, kvlib, case):
 def test_copy_prepared_matches_wrapper(gpu, kvlib, case):
     import torch
 
-    from radeon_kernels.workloads import make_copy_inputs
+    from benchmarks.workloads import make_copy_inputs
 
     data = make_copy_inputs(case, dtype="fp16", index_dtype="int32", device=gpu)
     announce(f"prepared copy {case}")
@@ -82,7 +82,7 @@ def test_sdpa_prepared_matches_wrapper(gpu, case):
     import torch
 
     from radeon_kernels.cabi import sdpa_library
-    from radeon_kernels.workloads import make_sdpa_inputs
+    from benchmarks.workloads import make_sdpa_inputs
 
     lib = sdpa_library()
     data = make_sdpa_inputs(case, dtype="fp16", device=gpu)

@@ -26,7 +26,7 @@ import torch
 
 from oracle import kv_oracle
 from radeon_kernels.ops.kv_cache.reference import kv_cache_append_reference
-from radeon_kernels.workloads import APPEND_CASES, make_append_inputs
+from benchmarks.workloads import APPEND_CASES, make_append_inputs
 
 
 def bits(t):
@@ -60,7 +60,7 @@ def test_oracle_matches_torch_index_copy(case, dtype, index_dtype):
 
 
 def small(seed=3, tokens=5, num_blocks=6, block_size=4, kv_heads=2, head_dim=8, index_dtype="int64"):
-    from radeon_kernels.workloads import AppendCase
+    from benchmarks.workloads import AppendCase
 
     return make_append_inputs(AppendCase("small", tokens, num_blocks, block_size, kv_heads, head_dim),
                               dtype="fp16", index_dtype=index_dtype, seed=seed)
@@ -159,7 +159,7 @@ def test_unmutated_restatement_passes_the_same_checks():
 # ---------------------------------------------------------------------------------------------
 # Block copy (reference.py:23-38)
 from radeon_kernels.ops.kv_cache.reference import kv_cache_copy_reference  # noqa: E402
-from radeon_kernels.workloads import COPY_CASES, CopyCase, make_copy_inputs  # noqa: E402
+from benchmarks.workloads import COPY_CASES, CopyCase, make_copy_inputs  # noqa: E402
 
 
 def copy_args(data):

@@ -247,7 +247,7 @@ def test_golden_tiny_cases_reproduce():
 
 
 def test_golden_c1_inputs_and_output_reproduce():
-    from radeon_kernels.workloads import make_inputs
+    from benchmarks.workloads import make_inputs
 
     golden = np.load(GOLDEN / "c1_expected.npz")
     data = make_inputs("c1")

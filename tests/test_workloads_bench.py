@@ -12,7 +12,7 @@ from pathlib import Path
 import pytest
 import torch
 
-from radeon_kernels.workloads import WORKLOADS, aux_bytes, kv_bytes, make_inputs
+from benchmarks.workloads import WORKLOADS, aux_bytes, kv_bytes, make_inputs
 
 ROOT = Path(__file__).resolve().parents[1]
 

@@ -175,6 +175,31 @@ int rk_pa_decode_append(const void* query, const void* new_key, const void* new_
                         int64_t max_blocks_per_sequence, float scale, int dtype, int index_dtype,
                         int64_t partition_tokens, int variant, void* stream);
 
+/*
+ * Allocation-free decode.  No counterpart in the reference: it exists for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as rk_pa_decode (the same two launches, so the
+ * output is bit-identical), minus the workspace: the split-K records go to a device array the
+ * library holds, RK_PA_NOALLOC_SCRATCH_BYTES bytes per GPU, from the first call on that GPU until
+ * the process ends.  The call makes no hipMalloc/hipFree or other allocating call; the first call
+ * on a device looks up that device's array address once.
+ *
+ * A shape whose rk_pa_decode_workspace_bytes exceeds RK_PA_NOALLOC_SCRATCH_BYTES is rejected with
+ * RK_ERR_WORKSPACE before anything is launched (a larger partition_tokens needs fewer records).
+ * The stream must belong to the current device (RK_ERR_INVALID_ARGUMENT otherwise).
+ *
+ * Every call on one GPU shares that GPU's array: calls that may overlap in time on one GPU
+ * (different streams, or different host threads without stream ordering) race on it and must be
+ * serialised by the caller.  Calls in one stream's order are safe.
+ */
+#define RK_PA_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+int rk_pa_decode_noalloc(const void* query, const void* key_cache, const void* value_cache,
+                         const void* block_tables, const void* context_lengths, void* output,
+                         int64_t batch, int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                         int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_sequence,
+                         float scale, int dtype, int index_dtype, int64_t partition_tokens,
+                         int variant, void* stream);
+
 /* Text describing the last non-RK_OK status returned on the calling thread. */
 const char* rk_pa_last_error(void);
 

@@ -36,6 +36,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "rk_paged_attention.h"
@@ -1210,10 +1211,55 @@ extern "C" int rk_pa_decode_counter_words(int64_t batch, int64_t query_heads, in
 
 namespace {
 
+// ---------------------------------------------------------------------------------------------
+// Allocation-free decode: rk_pa_decode with its split-K records in a library-owned device array.
+//
+// `scratch` is a file-scope device array; every GPU the library runs on holds its own copy (at its
+// own address) from the first call on that GPU until the process ends.  In host code the array's
+// name is only a host-side stand-in, never a device address: the device address is looked up once
+// per device with hipGetSymbolAddress, with that device current, and kept in g_scratch_ptr.  Only
+// that pointer ever reaches a kernel.  The two-launch form needs nothing zeroed: the partition
+// kernel writes every record the reduce kernel reads.
+static __device__ __align__(256) unsigned char scratch[RK_PA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 256;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of this device's `scratch`, looked up on the first call per device.
+int scratch_address(void* stream, void** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(RK_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (stream != nullptr) {
+    int stream_device = -1;
+    err = hipStreamGetDevice(static_cast<hipStream_t>(stream), &stream_device);
+    if (err != hipSuccess)
+      return fail(RK_ERR_INVALID_ARGUMENT, "hipStreamGetDevice failed: %s", hipGetErrorString(err));
+    if (stream_device != device)
+      return fail(RK_ERR_INVALID_ARGUMENT, "stream belongs to device %d but device %d is current",
+                  stream_device, device);
+  }
+  if (device < 0 || device >= kMaxDevices)
+    return fail(RK_ERR_UNSUPPORTED, "device index %d is outside [0, %d)", device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return fail(RK_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                  hipGetErrorString(err));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return RK_OK;
+}
+
 constexpr int kPhasePartitions = 1;
 constexpr int kPhaseReduce = 2;
 constexpr int kPhaseFused = 4;  // partition kernel merging in its last workgroups; no reduce launch
 constexpr int kPhaseAppend = 8; // partition kernel also writes each sequence's new token (AP)
+constexpr int kPhaseScratch = 16; // records in this device's `scratch` array, not `workspace`
 
 int decode_phases(const void* query, const void* key_cache, const void* value_cache,
                   const void* block_tables, const void* context_lengths, void* output, void* workspace,
@@ -1249,6 +1295,20 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   if (status != RK_OK) return status;
   s.num_partitions = partitions_for(s);
   const size_t need = workspace_for(s);
+  if ((phases & kPhaseScratch) != 0) {
+    if (need > RK_PA_NOALLOC_SCRATCH_BYTES)
+      return fail(RK_ERR_WORKSPACE,
+                  "this shape needs %zu bytes of split-K scratch; rk_pa_decode_noalloc holds %zu "
+                  "(use a larger partition_tokens, or rk_pa_decode with a workspace)",
+                  need, static_cast<size_t>(RK_PA_NOALLOC_SCRATCH_BYTES));
+    workspace = nullptr;
+    workspace_bytes = 0;
+    if (need > 0) {
+      status = scratch_address(stream, &workspace);
+      if (status != RK_OK) return status;
+      workspace_bytes = RK_PA_NOALLOC_SCRATCH_BYTES;
+    }
+  }
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(RK_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
                 workspace_bytes);
@@ -1393,6 +1453,19 @@ extern "C" int rk_pa_decode_append(const void* query, const void* new_key, const
                        num_blocks, block_size, max_blocks_per_sequence, scale, dtype, index_dtype,
                        partition_tokens, variant, stream, phases, counters, counter_words, new_key,
                        new_value);
+}
+
+extern "C" int rk_pa_decode_noalloc(const void* query, const void* key_cache, const void* value_cache,
+                                    const void* block_tables, const void* context_lengths, void* output,
+                                    int64_t batch, int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                                    int64_t num_blocks, int64_t block_size,
+                                    int64_t max_blocks_per_sequence, float scale, int dtype,
+                                    int index_dtype, int64_t partition_tokens, int variant,
+                                    void* stream) {
+  return decode_phases(query, key_cache, value_cache, block_tables, context_lengths, output, nullptr, 0,
+                       batch, query_heads, kv_heads, head_dim, num_blocks, block_size,
+                       max_blocks_per_sequence, scale, dtype, index_dtype, partition_tokens, variant,
+                       stream, kPhasePartitions | kPhaseReduce | kPhaseScratch);
 }
 
 extern "C" const char* rk_pa_last_error(void) { return g_last_error.c_str(); }

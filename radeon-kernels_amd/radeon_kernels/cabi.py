@@ -28,6 +28,7 @@ RK_DTYPE_FP16 = 0
 RK_DTYPE_BF16 = 1
 RK_INDEX_INT32 = 0
 RK_INDEX_INT64 = 1
+RK_PA_NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
 VARIANTS = {"mfma": 0, "valu": 1}
 
 EXPORTED_SYMBOLS = (
@@ -38,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "rk_pa_decode_fused",
     "rk_pa_decode_counter_words",
     "rk_pa_decode_workspace_bytes",
+    "rk_pa_decode_noalloc",
     "rk_pa_last_error",
     "rk_pa_version",
 )
@@ -86,6 +88,8 @@ class PagedAttentionLibrary:
         lib.rk_pa_decode_fused.restype = ctypes.c_int
         lib.rk_pa_decode_append.argtypes = [vp, vp, vp] + decode_args[1:8] + [vp, sz] + decode_args[8:]
         lib.rk_pa_decode_append.restype = ctypes.c_int
+        lib.rk_pa_decode_noalloc.argtypes = decode_args[:6] + decode_args[8:]
+        lib.rk_pa_decode_noalloc.restype = ctypes.c_int
         lib.rk_pa_decode_counter_words.argtypes = [i64, i64, i64, ctypes.POINTER(sz)]
         lib.rk_pa_decode_counter_words.restype = ctypes.c_int
         lib.rk_pa_last_error.argtypes = []
@@ -139,6 +143,44 @@ class PagedAttentionLibrary:
         if phase == "fused":
             return self.lib.rk_pa_decode_fused, (*head, counters or None, counter_words, *tail)
         return getattr(self.lib, PHASES[phase]), (*head, *tail)
+
+    def decode_noalloc_raw(self, *, query: int, key_cache: int, value_cache: int, block_tables: int,
+                           context_lengths: int, output: int, batch: int, query_heads: int, kv_heads: int,
+                           head_dim: int, num_blocks: int, block_size: int, max_blocks: int, scale: float,
+                           dtype: int, index_dtype: int, partition_tokens: int, variant: int, stream: int) -> int:
+        """rk_pa_decode_noalloc on raw device pointers; returns the status."""
+
+        return self.lib.rk_pa_decode_noalloc(query, key_cache, value_cache, block_tables, context_lengths, output,
+                                             batch, query_heads, kv_heads, head_dim, num_blocks, block_size,
+                                             max_blocks, ctypes.c_float(scale), dtype, index_dtype,
+                                             partition_tokens, variant, stream or None)
+
+    def decode_noalloc(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
+                       scale: float | None = None, *, out: Any, partition_tokens: int = 512, variant: str = "mfma",
+                       stream: Any | None = None) -> Any:
+        """rk_pa_decode_noalloc on torch tensors: writes ``out`` (caller-allocated) and returns it.
+
+        The split-K records live in the library's per-GPU scratch array, so nothing is allocated
+        here or in the library.
+        """
+
+        import torch
+
+        batch, query_heads, head_dim = (int(s) for s in query.shape)
+        num_blocks, block_size, kv_heads, _ = (int(s) for s in key_cache.shape)
+        if scale is None:
+            scale = 1.0 / math.sqrt(head_dim)
+        if stream is None:
+            stream = torch.cuda.current_stream(query.device)
+        self.check(self.decode_noalloc_raw(
+            query=query.data_ptr(), key_cache=key_cache.data_ptr(), value_cache=value_cache.data_ptr(),
+            block_tables=block_tables.data_ptr(), context_lengths=context_lengths.data_ptr(), output=out.data_ptr(),
+            batch=batch, query_heads=query_heads, kv_heads=kv_heads, head_dim=head_dim, num_blocks=num_blocks,
+            block_size=block_size, max_blocks=int(block_tables.shape[1]), scale=float(scale),
+            dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
+            index_dtype=RK_INDEX_INT64 if block_tables.dtype == torch.int64 else RK_INDEX_INT32,
+            partition_tokens=partition_tokens, variant=VARIANTS[variant], stream=stream.cuda_stream))
+        return out
 
     def decode_raw(self, **arguments: Any) -> int:
         """One launch on raw device pointers (the keywords of ``_raw_call``); returns the status."""

@@ -202,6 +202,55 @@ def test_last_error_is_per_thread(lib):
     assert "dtype" in lib.last_error()
 
 
+def test_noalloc_scratch_limit_matches_header():
+    text = HEADER.read_text()
+    match = re.search(r"#define RK_PA_NOALLOC_SCRATCH_BYTES \((\d+)u \* 1024u \* 1024u\)", text)
+    assert match and int(match.group(1)) * 1024 * 1024 == cabi.RK_PA_NOALLOC_SCRATCH_BYTES
+
+
+def noalloc_call(lib, **overrides):
+    args = dict(query=16, key_cache=32, value_cache=48, block_tables=64, context_lengths=80, output=96, batch=2,
+                query_heads=8, kv_heads=2, head_dim=128, num_blocks=8, block_size=16, max_blocks=4, scale=0.125,
+                dtype=cabi.RK_DTYPE_BF16, index_dtype=cabi.RK_INDEX_INT32, partition_tokens=64, variant=0, stream=0)
+    args.update(overrides)
+    return lib.decode_noalloc_raw(**args), lib.last_error()
+
+
+@cpu_only
+@pytest.mark.parametrize(
+    "overrides, status, message",
+    [
+        (dict(query=0), cabi.RK_ERR_INVALID_ARGUMENT, "must not be NULL"),
+        (dict(dtype=7), cabi.RK_ERR_INVALID_ARGUMENT, "dtype"),
+        (dict(head_dim=100), cabi.RK_ERR_INVALID_ARGUMENT, "head_dim"),
+        (dict(partition_tokens=24), cabi.RK_ERR_INVALID_ARGUMENT, "partition_tokens"),
+        # 4096 x 32 heads x 64 partitions of 16 tokens: 4096*32*64*(128+2)*4 bytes of records > 32 MiB.
+        (dict(batch=4096, query_heads=32, kv_heads=8, max_blocks=64, partition_tokens=16), cabi.RK_ERR_WORKSPACE,
+         "bytes of split-K scratch; rk_pa_decode_noalloc holds 33554432"),
+    ],
+)
+def test_noalloc_validates_like_decode_before_any_device_call(lib, overrides, status, message):
+    got, text = noalloc_call(lib, **overrides)
+    assert got == status, text
+    assert message in text
+
+
+@cpu_only
+def test_noalloc_scratch_limit_boundary(lib):
+    """The largest shape whose records fit is accepted by validation (it then needs a device: without
+    one the scratch lookup fails as a launch error); one more sequence is rejected."""
+
+    # records of b sequences x 32 heads x 16 partitions (P 64 over 1024 tokens): b*32*16*(128*4) + b*32*16*8
+    per_seq = 32 * 16 * 128 * 4 + 32 * 16 * 8
+    fit = cabi.RK_PA_NOALLOC_SCRATCH_BYTES // per_seq
+    assert lib.workspace_bytes(fit, 32, 128, 16, 64, 64) <= cabi.RK_PA_NOALLOC_SCRATCH_BYTES
+    assert lib.workspace_bytes(fit + 1, 32, 128, 16, 64, 64) > cabi.RK_PA_NOALLOC_SCRATCH_BYTES
+    got, text = noalloc_call(lib, batch=fit + 1, query_heads=32, kv_heads=8, max_blocks=64)
+    assert got == cabi.RK_ERR_WORKSPACE, text
+    got, text = noalloc_call(lib, batch=fit, query_heads=32, kv_heads=8, max_blocks=64)
+    assert got == cabi.RK_ERR_LAUNCH and "hipGetDevice" in text, text
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(FileNotFoundError, match="build"):
         cabi.PagedAttentionLibrary(tmp_path / "absent.so")

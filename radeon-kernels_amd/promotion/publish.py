@@ -23,10 +23,12 @@ and all in the reference's formats:
 What differs from the reference's flow, deliberately:
 
 * the approval is automated and says so: reviewer ``rk-gfx950-build-gates``, a reason stating that
-  every deterministic gate passed and that it is not a human release decision.  The records are
-  signed with this build's development key (``rk-gfx950-dev``, generated on first use and kept in
-  ``.signing/``, which is never committed); a maintainer approves and re-signs with a release key
-  to publish alongside the reference's packs;
+  every deterministic gate passed and that it is not a human release decision.  The pack and the
+  records are signed with the gfx950 release key ``rk-gfx950-release-2026-12``, whose public half
+  the built-in keyring ships and whose private half stays in ``.signing/`` (never committed;
+  created once by ``publish.py --create-release-key``).  A machine without it signs with its own
+  development key, trusted only by a process that names ``.signing/dev-trusted-keys.json`` in
+  RADEON_KERNELS_DEV_TRUSTED_KEYS; this tool never writes the built-in keyring after set-up;
 * one pack holds all three operators, so each operator has one evidence record covering all of its
   exact dispatch entries (correctness cases for each, timing on the headline workload), where the
   reference builds one pack and one evidence record per workload.
@@ -59,13 +61,16 @@ from radeon_kernels.errors import ConfigError  # noqa: E402
 from radeon_kernels.runtime.ed25519 import Ed25519PrivateKey  # noqa: E402
 from radeon_kernels.runtime.signing import (  # noqa: E402
     BUILTIN_KEYRING,
+    DEV_KEYRING_ENV,
     TrustedKey,
     TrustedKeyring,
     signature_document,
 )
 
+RELEASE_KEY_ID = "rk-gfx950-release-2026-12"
 DEV_KEY_ID = "rk-gfx950-dev"
 KEY_DIR = PACKAGE_ROOT / ".signing"
+DEV_KEYRING = KEY_DIR / "dev-trusted-keys.json"
 PACK_DIR = PACKAGE_ROOT / "packs" / "gfx950"
 EVALUATIONS = PACKAGE_ROOT / "evaluations"
 RECORD_DIRS = {name: PACKAGE_ROOT / name for name in ("proposals", "approvals", "evidence", "pack-index")}
@@ -74,8 +79,9 @@ OPERATORS = ("paged_attention_decode", "kv_cache_append", "kv_cache_copy", "sdpa
 MINIMUM_IMPROVEMENT_PCT = 3.0
 MAXIMUM_CV = 0.03
 REVIEWER = "rk-gfx950-build-gates"
-DEV_KEY_REASON = ("development key of the gfx950 build: signs its pack manifest and automated promotion "
-                  "records; not a release key")
+DEV_KEY_REASON = ("development key of one gfx950 build machine: trusted only through "
+                  "RADEON_KERNELS_DEV_TRUSTED_KEYS; not a release key")
+RELEASE_KEY_REASON = "release key of the gfx950 pack: signs its manifest and its promotion records"
 
 
 def _sha256(data: bytes) -> str:
@@ -124,36 +130,61 @@ def generate_private_key(path: Path, key_id: str) -> None:
         json.dump(document, stream, indent=2, sort_keys=True)
 
 
-def development_key() -> Ed25519PrivateKey:
-    """The build's signing key, created on first use; its public half is made the active
-    ``rk-gfx950-dev`` entry of the built-in keyring (an earlier development key is kept, revoked)."""
+def _public_b64(key: Ed25519PrivateKey) -> str:
+    return base64.b64encode(key.public_key().public_bytes()).decode("ascii")
 
+
+def signing_key() -> tuple[str, Ed25519PrivateKey]:
+    """(key_id, key) that signs the pack and the promotion records.
+
+    The release key ``rk-gfx950-release-2026-12`` when its private half is present in ``.signing/``
+    and matches the public key the built-in keyring ships; otherwise this machine's development key
+    (created on first use), whose public half goes to ``.signing/dev-trusted-keys.json`` only.  The
+    built-in keyring (radeon_kernels/keys/trusted-keys.json) is never written here: a pack signed with
+    a development key loads only in a process that sets RADEON_KERNELS_DEV_TRUSTED_KEYS to that file.
+    """
+
+    release = KEY_DIR / f"{RELEASE_KEY_ID}.private.json"
+    if release.is_file():
+        key_id, key, _ = load_private_key(release)
+        shipped = {entry.key_id: entry for entry in TrustedKeyring.from_file(BUILTIN_KEYRING).keys}
+        entry = shipped.get(key_id)
+        if entry is None or entry.status != "active" or entry.public_key != key.public_key().public_bytes():
+            raise ConfigError(str(release), "release key does not match the active key the built-in keyring ships")
+        return key_id, key
     path = KEY_DIR / f"{DEV_KEY_ID}.private.json"
     if not path.is_file():
         generate_private_key(path, DEV_KEY_ID)
     key_id, key, created_at = load_private_key(path)
-    public = key.public_key().public_bytes()
+    dev_ring = TrustedKeyring([TrustedKey(key_id, key.public_key().public_bytes(), "active", created_at,
+                                          DEV_KEY_REASON)])
+    _write(DEV_KEYRING, _json_bytes(dev_ring.to_dict()))
+    sys.stderr.write(f"warning: no release key in {KEY_DIR}; the pack is signed with the development key {key_id} "
+                     f"and loads only with {DEV_KEYRING_ENV}={DEV_KEYRING}\n")
+    return key_id, key
+
+
+def create_release_key() -> str:
+    """One-time set-up of the gfx950 release key: its private half goes to ``.signing/`` (never
+    committed) and its public half is added to the built-in keyring.  Refuses to replace a key."""
+
+    path = KEY_DIR / f"{RELEASE_KEY_ID}.private.json"
     keyring = TrustedKeyring.from_file(BUILTIN_KEYRING)
-    keys = []
-    for entry in keyring.keys:
-        if entry.key_id == key_id and entry.public_key != public:
-            # A replaced development key stays listed under a dated id, revoked.
-            stamp = entry.created_at[:19].replace("-", "").replace(":", "").lower()
-            keys.append(TrustedKey(f"{key_id}-{stamp}", entry.public_key, "revoked", entry.created_at,
-                                   "replaced development key"))
-        elif entry.key_id != key_id:
-            keys.append(entry)
-    keys.append(TrustedKey(key_id, public, "active", created_at, DEV_KEY_REASON))
-    ordered = sorted(keys, key=lambda item: (item.key_id != "rk-release-2026-09", item.key_id))
-    _write(BUILTIN_KEYRING, _json_bytes(TrustedKeyring(ordered).to_dict()))
-    return key
+    if any(entry.key_id == RELEASE_KEY_ID for entry in keyring.keys) or path.exists():
+        raise ConfigError(RELEASE_KEY_ID, "the release key already exists; rotate it by hand, not by this tool")
+    generate_private_key(path, RELEASE_KEY_ID)
+    key_id, key, created_at = load_private_key(path)
+    keys = [entry for entry in keyring.keys]
+    keys.append(TrustedKey(key_id, key.public_key().public_bytes(), "active", created_at, RELEASE_KEY_REASON))
+    _write(BUILTIN_KEYRING, _json_bytes(TrustedKeyring(keys).to_dict()))
+    return _public_b64(key)
 
 
-def sign(path: Path, key: Ed25519PrivateKey, signed_file: str | None = None) -> Path:
+def sign(path: Path, key_id: str, key: Ed25519PrivateKey, signed_file: str | None = None) -> Path:
     """Write ``<stem>.sig.json`` beside ``path`` (``manifest.sig.json`` for ``manifest.json``)."""
 
     name = signed_file or path.name
-    document = signature_document(private_key=key, key_id=DEV_KEY_ID, signed_file=name,
+    document = signature_document(private_key=key, key_id=key_id, signed_file=name,
                                   signed_sha256=_sha256(path.read_bytes()))
     target = path.with_name(path.name[: -len(".json")] + ".sig.json")
     _write(target, _json_bytes(document))
@@ -328,9 +359,9 @@ def release_archive(pack_id: str, pack_version: str, files: list[str]) -> Path:
 def publish(verbose: bool = False) -> dict[str, str]:
     """Sign the pack and (re)write every promotion record; returns operator -> decision."""
 
-    key = development_key()
+    key_id, key = signing_key()
     manifest_path = PACK_DIR / "manifest.json"
-    manifest_sig = sign(manifest_path, key)
+    manifest_sig = sign(manifest_path, key_id, key)
     manifest = json.loads(manifest_path.read_text(encoding="utf-8"))
     archive = release_archive(manifest["pack_id"], manifest["pack_version"],
                               ["manifest.json", "manifest.sig.json", *[a["artifact"] for a in manifest["artifacts"]]])
@@ -360,7 +391,7 @@ def publish(verbose: bool = False) -> dict[str, str]:
             "reviewer": REVIEWER,
             "reviewed_at": proposal["created_at"],
             "reason": ("Automated approval by the gfx950 build: every deterministic promotion gate passed ("
-                       + ", ".join(proposal["gates"]) + f"). Signed with the development key {DEV_KEY_ID}; "
+                       + ", ".join(proposal["gates"]) + f"). Signed with {key_id}; "
                        "not a human release decision."),
         }
         evidence = dict(proposal["public_evidence"], approval_id=approval_id)
@@ -386,7 +417,7 @@ def publish(verbose: bool = False) -> dict[str, str]:
                                           ("pack-index", f"{operator}-1.0", index)):
             path = RECORD_DIRS[directory] / f"{name}.json"
             _write(path, _json_bytes(document))
-            keep.update({path, sign(path, key)})
+            keep.update({path, sign(path, key_id, key)})
     for directory in RECORD_DIRS.values():
         for stale in directory.glob("*.json") if directory.is_dir() else ():
             if stale not in keep:
@@ -397,4 +428,7 @@ def publish(verbose: bool = False) -> dict[str, str]:
 
 
 if __name__ == "__main__":
-    publish(verbose=True)
+    if sys.argv[1:] == ["--create-release-key"]:
+        print(f"created {RELEASE_KEY_ID}: public key {create_release_key()}")
+    else:
+        publish(verbose=True)

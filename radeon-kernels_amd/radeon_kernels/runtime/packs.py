@@ -8,7 +8,8 @@ environment matches the fingerprint and whose artifact record equals the dispatc
 
 Signatures are required by default, as in the reference (packs.py:88-113): every pack's
 ``manifest.json`` must carry a ``manifest.sig.json`` that verifies under the trusted keyring
-(radeon_kernels.runtime.signing; the built-in keyring unless one is given), else the pack is
+(radeon_kernels.runtime.signing; the built-in release keyring, plus the development keyring an
+opt-in environment variable names, unless a keyring is given), else the pack is
 rejected with the reason.
 
 One deliberate difference: the in-tree pack directory written by the build
@@ -31,7 +32,7 @@ from radeon_kernels.runtime.registry import ArtifactSpec
 from radeon_kernels.runtime.signing import (
     SignatureVerificationError,
     TrustedKeyring,
-    builtin_trusted_keyring,
+    default_trusted_keyring,
     verify_detached_file,
 )
 
@@ -104,7 +105,7 @@ class KernelPackRegistry:
         rejected: list[str] = []
         keyring = trusted_keys
         if require_signatures and keyring is None:
-            keyring = builtin_trusted_keyring()
+            keyring = default_trusted_keyring()
         for directory in pack_directories(roots):
             try:
                 if require_signatures:

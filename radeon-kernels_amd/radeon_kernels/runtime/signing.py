@@ -27,6 +27,7 @@ import base64
 import hashlib
 import hmac
 import json
+import os
 import re
 from collections.abc import Mapping, Sequence
 from dataclasses import dataclass
@@ -252,4 +253,29 @@ def verify_detached_file(file_path: Path, signature_path: Path, keyring: Trusted
 
 
 def builtin_trusted_keyring() -> TrustedKeyring:
+    """The release keys shipped with the package (never rewritten by a build)."""
+
     return TrustedKeyring.from_file(BUILTIN_KEYRING)
+
+
+# A keyring file of development keys, trusted in addition to the built-in release keys only when this
+# environment variable names it: packs signed on a build machine without a release key load only for a
+# process that opts in.
+DEV_KEYRING_ENV = "RADEON_KERNELS_DEV_TRUSTED_KEYS"
+
+
+def default_trusted_keyring(environ: Mapping[str, str] | None = None) -> TrustedKeyring:
+    """The built-in keyring, plus the development keyring named by ``RADEON_KERNELS_DEV_TRUSTED_KEYS``.
+
+    A development keyring may add keys but never replace or shadow a built-in key id.
+    """
+
+    builtin = builtin_trusted_keyring()
+    path = (os.environ if environ is None else environ).get(DEV_KEYRING_ENV, "")
+    if not path:
+        return builtin
+    extra = TrustedKeyring.from_file(Path(path))
+    clash = sorted({key.key_id for key in builtin.keys} & {key.key_id for key in extra.keys})
+    if clash:
+        raise ConfigError(f"{DEV_KEYRING_ENV}={path}", f"development keyring redefines built-in key ids {clash}")
+    return TrustedKeyring([*builtin.keys, *extra.keys])

@@ -213,12 +213,66 @@ def test_schema_checker_catches_planted_violations(mutation, fragment):
 
 # ---------------------------------------------------------------------------------------------
 # This build's keyring and signed records.
-def test_builtin_keyring_holds_the_reference_release_key_and_the_gfx950_development_key():
+def test_builtin_keyring_holds_release_keys_only():
+    """The shipped trust root: the reference's release key and the gfx950 release key, nothing else
+    (no development key of any build machine)."""
+
     keyring = builtin_trusted_keyring()
     assert not _schema.errors(keyring.to_dict(), schema("trusted-keys"))
     keys = {key.key_id: key for key in keyring.keys}
+    assert sorted(keys) == ["rk-gfx950-release-2026-12", "rk-release-2026-09"]
     assert keys["rk-release-2026-09"].public_key == reference_keyring().keys[0].public_key
-    assert keys["rk-gfx950-dev"].status == "active" and "not a release key" in keys["rk-gfx950-dev"].reason
+    assert keys["rk-gfx950-release-2026-12"].status == "active"
+    assert all("development" not in (key.reason or "") for key in keys.values())
+
+
+def _dev_keyring_file(tmp_path, key_id="rk-dev-test"):
+    key = ed25519.Ed25519PrivateKey.from_private_bytes(bytes(range(32)))
+    ring = TrustedKeyring([TrustedKey(key_id, key.public_key().public_bytes(), "active", "2026-12-02")])
+    path = tmp_path / "dev-trusted-keys.json"
+    path.write_text(json.dumps(ring.to_dict()))
+    return path, key
+
+
+def test_development_keyring_is_trusted_only_on_opt_in(tmp_path):
+    from radeon_kernels.runtime.signing import DEV_KEYRING_ENV, default_trusted_keyring
+
+    path, key = _dev_keyring_file(tmp_path)
+    assert {k.key_id for k in default_trusted_keyring(environ={}).keys} == \
+        {k.key_id for k in builtin_trusted_keyring().keys}
+    merged = default_trusted_keyring(environ={DEV_KEYRING_ENV: str(path)})
+    assert merged.active_public_key("rk-dev-test").public_bytes() == key.public_key().public_bytes()
+    assert merged.active_public_key("rk-release-2026-09")  # built-in keys stay
+    (tmp_path / "clash").mkdir()
+    clash, _ = _dev_keyring_file(tmp_path / "clash", key_id="rk-release-2026-09")
+    with pytest.raises(ConfigError, match="redefines built-in key ids"):
+        default_trusted_keyring(environ={DEV_KEYRING_ENV: str(clash)})
+
+
+def test_a_build_without_the_release_key_never_touches_the_builtin_keyring(tmp_path, monkeypatch):
+    """publish.signing_key() on a machine without the release key: a development key signs, its public
+    half goes to the machine's own dev keyring, and the shipped keyring's bytes are unchanged."""
+
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("rk_publish_under_test", PACKAGE / "promotion" / "publish.py")
+    publish = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(publish)
+    before = publish.BUILTIN_KEYRING.read_bytes()
+    monkeypatch.setattr(publish, "KEY_DIR", tmp_path / "signing")
+    monkeypatch.setattr(publish, "DEV_KEYRING", tmp_path / "signing" / "dev-trusted-keys.json")
+    key_id, key = publish.signing_key()
+    assert key_id == "rk-gfx950-dev"
+    assert publish.BUILTIN_KEYRING.read_bytes() == before
+    dev = TrustedKeyring.from_file(tmp_path / "signing" / "dev-trusted-keys.json")
+    assert dev.active_public_key(key_id).public_bytes() == key.public_key().public_bytes()
+    with pytest.raises(SignatureVerificationError, match="unknown key"):
+        builtin_trusted_keyring().active_public_key(key_id)
+    with pytest.raises(ConfigError, match="already exists"):
+        monkeypatch.setattr(publish, "KEY_DIR", tmp_path / "other")
+        (tmp_path / "other").mkdir()
+        publish.create_release_key()  # the shipped keyring already holds the release key id
+    assert publish.BUILTIN_KEYRING.read_bytes() == before
 
 
 def _records(directory: str) -> list[Path]:
@@ -288,7 +342,7 @@ def test_pack_index_records_name_this_pack_and_its_release_archive():
                 assert handle.extractfile(member).read() == (pack / member.name.split("/", 1)[1]).read_bytes()
 
 
-def test_development_key_stays_out_of_the_repository_history():
+def test_signing_keys_stay_out_of_the_repository_history():
     ignore = (PACKAGE.parent / ".gitignore").read_text()
     assert "radeon-kernels_amd/.signing/" in ignore
     key_dir = PACKAGE / ".signing"

@@ -57,7 +57,9 @@ def parse_args(argv=None):
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--workload", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--workload", default="c5",
+                        help="c1..c5 (the five measured shapes) or one of the reference's decode cases, "
+                             "<case id>-<fp16|bf16> (benchmarks/workloads/paged_attention_decode-1.0.yaml)")
     parser.add_argument("--variant", default=None, choices=["mfma", "valu"])
     parser.add_argument("--partition", type=int, default=None)
     parser.add_argument("--merge", default=None, choices=["fused", "reduce"],
@@ -125,23 +127,27 @@ def settle(torch, launch, copies: int = 1, seconds: float = SETTLE_SECONDS, limi
             break
 
 
-def dispatch_launch(workload_key: str) -> tuple[str, int, str]:
-    """Entrypoint, partition size and merge form the gfx950 dispatch table assigns to this workload."""
+def dispatch_launch(torch, q, k, v, bt, cl) -> dict:
+    """The dispatch decision of the public operator on these inputs (entry id, entrypoint, launch
+    parameters), from one call that must run natively."""
 
-    from radeon_kernels import dispatch_plan
+    import warnings
 
-    names = {"c1": "b1-gqa32x8-c128-d128-p16-fp16", "c2": "b8-gqa32x8-c1024-d128-p16-bf16",
-             "c3": "b4-mha16-c2048-d64-p32-bf16", "c4": "b4-gqa32x8-c1024-d256-p16-fp16",
-             "c5": "b128-gqa32x8-ragged-d128-p16-bf16"}
-    for suffix, _, launch in dispatch_plan.EXACT_REGIONS:
-        if suffix == names[workload_key]:
-            return dispatch_plan.ENTRYPOINT, int(launch["partition_tokens"]), str(launch["merge"])
-    raise KeyError(workload_key)
+    import radeon_kernels as rk
+    from radeon_kernels.ops._runtime import NativeDemotionWarning
+
+    with warnings.catch_warnings():
+        # A demotion would run the torch fallback (tens of GB of intermediates on the largest workload).
+        warnings.simplefilter("error", NativeDemotionWarning)
+        rk.paged_attention_decode(q, k, v, bt, cl)
+    torch.cuda.synchronize()
+    return rk.get_last_dispatch()
 
 
-def read_traffic(workload: str, variant: str, partition: int, merge: str = "reduce"):
-    """HBM bytes per partition-kernel launch from the committed counter summary, if it matches
-    (``merge``: the form the summary was measured in; a summary without the field is "reduce")."""
+def read_traffic(workload: str, variant: str, partition: int, merge: str, kv_bytes: int):
+    """HBM bytes per partition-kernel launch from the committed counter summary, if it was measured
+    on exactly this configuration: workload, variant, partition size, merge form and the same input
+    draw (its KV bytes per call)."""
 
     if not TRAFFIC_SUMMARY.is_file():
         return None
@@ -152,7 +158,8 @@ def read_traffic(workload: str, variant: str, partition: int, merge: str = "redu
             fields[key.strip()] = value.strip()
     try:
         if (fields.get("workload") != workload or fields.get("variant") != variant
-                or int(fields["partition_tokens"]) != partition or fields.get("merge", "reduce") != merge):
+                or int(fields["partition_tokens"]) != partition or fields.get("merge", "reduce") != merge
+                or int(fields["kv_bytes_per_call"]) != kv_bytes):
             return None
         return int(fields["hbm_bytes_per_launch"])
     except (KeyError, ValueError):
@@ -190,22 +197,42 @@ def read_case_traffic(summary: Path, workload: str):
         return None
 
 
+def cpu_threads() -> tuple[int, int]:
+    """(threads used, cores in this process's affinity mask).  The thread count is the affinity mask,
+    capped by OMP_NUM_THREADS where the machine sets it to the job's CPU share."""
+
+    affinity = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(affinity, int(share)) if share.isdigit() and int(share) > 0 else affinity
+    return threads, affinity
+
+
 def cpu_baseline(torch, data, seconds: float) -> dict:
-    """Reference algorithm on the host cores over the first sequences of the workload."""
+    """The reference algorithm (its torch fallback, restated in oracle/) on the host cores.
+
+    Protocol: torch's CPU thread count is set to ``cpu_threads()``; the sample is the first
+    sequences of the workload whose rows one pass covers in about ``seconds / 4`` (the whole batch
+    for the small workloads), evaluated two sequences at a time; one untimed warmup pass, then three
+    timed passes (more for passes under 0.5 s, up to ``seconds`` in total and 30 passes); the reported rate is the
+    median pass.  K/V rows of the sample are gathered on the device and copied to the host before
+    timing, so the timed region is the fallback alone.
+    """
+
+    import statistics
 
     from oracle import pa_oracle
 
-    threads = torch.get_num_threads()
+    threads, affinity = cpu_threads()
+    torch.set_num_threads(threads)
     w = data["workload"]
     bt_all = data["block_tables"].cpu().to(torch.int64)
     ctx_all = data["context_lengths"].cpu().to(torch.int64)
     batch = bt_all.shape[0]
-    done, elapsed, kv_done, tokens_done = 0, 0.0, 0, 0
+    cap = w.max_blocks * w.block_size
     chunk = 2
-    while done < batch and elapsed < seconds:
-        rows = list(range(done, min(batch, done + chunk)))
-        bt = bt_all[rows]
-        ctx = ctx_all[rows]
+
+    def prepared_chunk(rows):
+        bt, ctx = bt_all[rows], ctx_all[rows]
         need = [min(math.ceil(int(c) / w.block_size), w.max_blocks) for c in ctx]
         used = torch.cat([bt[i, : need[i]] for i in range(len(rows))])
         remap = {int(b): i for i, b in enumerate(used.tolist())}
@@ -213,24 +240,45 @@ def cpu_baseline(torch, data, seconds: float) -> dict:
         for i in range(len(rows)):
             compact[i, : need[i]] = torch.tensor([remap[int(b)] for b in bt[i, : need[i]]])
         index = used.to(data["key_cache"].device)
-        k = data["key_cache"].index_select(0, index).cpu()
-        v = data["value_cache"].index_select(0, index).cpu()
-        q = data["query"][rows].cpu()
+        return (data["query"][rows].cpu(), data["key_cache"].index_select(0, index).cpu(),
+                data["value_cache"].index_select(0, index).cpu(), compact.to(torch.int32), ctx.to(torch.int32))
+
+    def run(chunks) -> float:
         start = time.perf_counter()
-        pa_oracle.fallback_restated(torch, q, k, v, compact.to(torch.int32), ctx.to(torch.int32))
-        elapsed += time.perf_counter() - start
+        for q, k, v, bt, ctx in chunks:
+            pa_oracle.fallback_restated(torch, q, k, v, bt, ctx)
+        return time.perf_counter() - start
+
+    # Size the sample: add chunks until one untimed pass over them takes seconds / 4 (this pass is
+    # the warmup).
+    chunks, warm, done = [], 0.0, 0
+    while done < batch and warm < seconds / 4:
+        rows = list(range(done, min(batch, done + chunk)))
+        prepared = prepared_chunk(rows)
+        warm += run([prepared])
+        chunks.append(prepared)
         done += len(rows)
-        tokens_done += int(sum(min(int(c), w.max_blocks * w.block_size) for c in ctx))
-    kv_done = tokens_done * w.kv_heads * w.head_dim * 2 * w.elem_size
-    gbps = kv_done / elapsed / 1e9
+    tokens = int(sum(min(int(c), cap) for c in ctx_all[:done]))
+    kv = tokens * w.kv_heads * w.head_dim * 2 * w.elem_size
+    passes = [run(chunks) for _ in range(3)]
+    while sum(passes) + warm < seconds and statistics.median(passes) < 0.5 and len(passes) < 30:
+        passes.append(run(chunks))
+    per_pass = statistics.median(passes)
+    gbps = kv / per_pass / 1e9
+    info = torch.__config__.parallel_info().splitlines()
     return {
         "value": round(gbps, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"first {done} of {batch} sequences ({tokens_done} context tokens, {kv_done / 1e9:.3f} GB of K/V), "
-                   f"evaluated {chunk} sequences at a time by the reference's torch fallback restated in "
-                   f"oracle/pa_oracle.py (torch {torch.__version__} CPU, {threads} threads), {elapsed:.1f} s"),
+        "sample": (f"first {done} of {batch} sequences ({tokens} context tokens, {kv / 1e9:.4f} GB of K/V) per "
+                   f"pass, {chunk} sequences at a time, by the reference's torch fallback restated in "
+                   f"oracle/pa_oracle.py (torch {torch.__version__} CPU, {threads} threads); 1 warmup pass, "
+                   f"median of {len(passes)} timed passes"),
+        "pass_seconds": {"passes": len(passes), "median": round(per_pass, 4), "min": round(min(passes), 4),
+                         "max": round(max(passes), 4)},
+        "affinity_cores": affinity,
+        "parallel_info": [line.strip() for line in info if line.strip()][:8],
         "us_per_call_extrapolated": round(data["kv_bytes"] / (gbps * 1e9) * 1e6, 1),
     }
 
@@ -522,16 +570,22 @@ def main(argv=None) -> int:
     device = torch.device("cuda:0")
     arch = torch.cuda.get_device_properties(0).gcnArchName.split(":", 1)[0]
     lib = library()  # raises if the HIP library was not built
+    if args.workload not in WORKLOADS:
+        print(json.dumps({"error": f"unknown workload {args.workload!r}", "workloads": sorted(WORKLOADS)}))
+        return 2
     w = WORKLOADS[args.workload]
-    entrypoint, planned_partition, planned_merge = dispatch_launch(args.workload)
-    variant = args.variant or entrypoint.split("_", 1)[1]
-    partition = args.partition or planned_partition
-    merge = args.merge or planned_merge
 
     if args.calibration_copy:
         calibration_copy(torch, device)
 
     data = make_inputs(w, device=device)
+    decision = dispatch_launch(torch, data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
+                               data["context_lengths"])
+    variant = args.variant or decision["selected"].split("/", 1)[1].split("_", 1)[1]  # native/decode_<variant>
+    partition = args.partition or int(decision["launch"]["partition_tokens"])
+    merge = args.merge or str(decision["launch"]["merge"])
+    if merge == "auto":  # the broad region's choice: fused below 4096 workgroups
+        merge = "fused"
     kv_bytes = data["kv_bytes"]
     cache_bytes = data["key_cache"].numel() * 2 * 2
     # Small workloads fit in the 256 MB last-level cache: rotate among enough K/V copies that each
@@ -617,17 +671,9 @@ def main(argv=None) -> int:
 
     # The public operator end to end (validation, dispatch, pack lookup, output and workspace
     # allocation, both launches) on the same inputs, back to back.
-    import warnings
-
     import radeon_kernels as rk
-    from radeon_kernels.ops._runtime import NativeDemotionWarning
 
     k, v = caches[0]
-    with warnings.catch_warnings():
-        # A demotion would run the torch fallback (tens of GB of intermediates at this size).
-        warnings.simplefilter("error", NativeDemotionWarning)
-        rk.paged_attention_decode(q, k, v, bt, cl)
-    decision = rk.get_last_dispatch()
     rk_us = public_call_us(torch, lambda: rk.paged_attention_decode(q, k, v, bt, cl), max(1, args.steps // 5))
 
     step = None
@@ -671,7 +717,7 @@ def main(argv=None) -> int:
                 "us_per_step_one_launch": round(one, 2), "entrypoints": ["rk_kv_cache_append + " + PHASE_SYMBOL[headline],
                                                                          "rk_pa_decode_append"]}
 
-    traffic = read_traffic(w.name, variant, partition, merge)
+    traffic = read_traffic(w.name, variant, partition, merge, kv_bytes)
     result = {
         "metric": METRIC,
         "value": round(gbps, 1),
@@ -684,7 +730,9 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": w.dtype,
-        "data": "synthetic (seeded N(0,1) query/K/V, seeded block tables and context lengths)",
+        "data": ("synthetic (seeded U(-0.125, 0.125) query/K/V as the reference benchmark draws them, seeded block "
+                 "tables)" if w.distribution == "uniform" else
+                 "synthetic (seeded N(0,1) query/K/V, seeded block tables and context lengths, drawn on the CPU)"),
         "config": {
             "workload": w.name,
             "batch": int(batch), "query_heads": int(hq), "kv_heads": int(hkv), "head_dim": int(d),

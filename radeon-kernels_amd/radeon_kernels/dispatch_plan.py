@@ -7,8 +7,9 @@ regions get which entrypoint and launch parameters -- is this table.
 
 Operators and regions:
 
-* ``paged_attention_decode``: one exact entry (priority 100) per measured workload shape, with the
-  partition size chosen for that shape (``launch.partition_tokens``) and how its partition records
+* ``paged_attention_decode``: one exact entry (priority 100) per case of the reference's workload file
+  in each dtype, plus the 128-sequence ragged shape, with the partition size chosen for that shape
+  (``launch.partition_tokens``) and how its partition records
   are merged (``launch.merge``: ``fused`` -- the partition kernel's last workgroup per sequence and
   head slot merges, one launch -- measured 7-12% faster on the 256-workgroup shapes; ``reduce`` -- a
   separate reduce launch, 0.5% faster on the 8192-workgroup ragged batch), and one broad gfx950
@@ -53,32 +54,53 @@ SDPA_ARTIFACT = "lib/rk_sdpa_gfx950.so"
 _INT_MAX = 2**31 - 1
 _POW2_BLOCKS = [1, 2, 4, 8, 16, 32, 64, 128, 256]
 
+# The reference's paged-decode workload cases (benchmarks/workloads/paged_attention_decode-1.0.yaml:13-22),
+# each in fp16 and bf16: id, batch, query heads, KV heads, context, head_dim, block size.  An entry
+# fixes every shape field but num_blocks (the cache size does not change the launch), so it also
+# covers the measured b1 / b8 / b4 shapes whose caches hold more blocks than their tables use.
+REFERENCE_CASES: list[tuple[str, int, int, int, int, int, int]] = [
+    ("b1-gqa32x8-c128-d128-p16", 1, 32, 8, 128, 128, 16),
+    ("b1-gqa32x8-c1024-d128-p16", 1, 32, 8, 1024, 128, 16),
+    ("b1-gqa32x8-c4096-d128-p16", 1, 32, 8, 4096, 128, 16),
+    ("b8-gqa32x8-c128-d128-p16", 8, 32, 8, 128, 128, 16),
+    ("b8-gqa32x8-c1024-d128-p16", 8, 32, 8, 1024, 128, 16),
+    ("b16-gqa32x8-c2048-d128-p16", 16, 32, 8, 2048, 128, 16),
+    ("b4-mha16-c2048-d64-p32", 4, 16, 16, 2048, 64, 32),
+    ("b4-gqa32x8-c1024-d256-p16", 4, 32, 8, 1024, 256, 16),
+]
+
+# Launch parameters per reference case (both dtypes): partition size and merge form, the fastest whole
+# call of a sweep of every case and dtype over partition sizes 16..4096 in both merge forms on MI355X,
+# with K/V rotated over enough copies to read from HBM.  The fused merge won every case; both dtypes
+# chose the same partition size (b1 c128 bf16 ties at 128 and 256).
+_CASE_PARTITION = {
+    "b1-gqa32x8-c128-d128-p16": 128,    # one partition: no merge at all
+    "b1-gqa32x8-c1024-d128-p16": 128,
+    "b1-gqa32x8-c4096-d128-p16": 256,
+    "b8-gqa32x8-c128-d128-p16": 128,    # one partition
+    "b8-gqa32x8-c1024-d128-p16": 256,
+    "b16-gqa32x8-c2048-d128-p16": 1024,
+    "b4-mha16-c2048-d64-p32": 512,
+    "b4-gqa32x8-c1024-d256-p16": 128,
+}
+REFERENCE_LAUNCH: dict[tuple[str, str], dict[str, Any]] = {
+    (case[0], dtype): {"partition_tokens": _CASE_PARTITION[case[0]], "merge": "fused"}
+    for case in REFERENCE_CASES for dtype in ("fp16", "bf16")
+}
+
+
+def _reference_region(case: tuple[str, int, int, int, int, int, int], dtype: str) -> dict[str, Any]:
+    _, batch, hq, hkv, context, head_dim, block_size = case
+    return {"dtype": dtype, "batch": batch, "query_heads": hq, "kv_heads": hkv, "head_dim": head_dim,
+            "num_blocks": [1, _INT_MAX], "block_size": block_size,
+            "max_blocks_per_sequence": -(-context // block_size)}
+
+
 # (id suffix, workload constraints, launch parameters)
 EXACT_REGIONS: list[tuple[str, dict[str, Any], dict[str, Any]]] = [
-    (
-        "b1-gqa32x8-c128-d128-p16-fp16",
-        {"dtype": "fp16", "batch": 1, "query_heads": 32, "kv_heads": 8, "head_dim": 128, "num_blocks": 64,
-         "block_size": 16, "max_blocks_per_sequence": 8},
-        {"partition_tokens": 128, "merge": "fused"},
-    ),
-    (
-        "b8-gqa32x8-c1024-d128-p16-bf16",
-        {"dtype": "bf16", "batch": 8, "query_heads": 32, "kv_heads": 8, "head_dim": 128, "num_blocks": 1024,
-         "block_size": 16, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 256, "merge": "fused"},
-    ),
-    (
-        "b4-mha16-c2048-d64-p32-bf16",
-        {"dtype": "bf16", "batch": 4, "query_heads": 16, "kv_heads": 16, "head_dim": 64, "num_blocks": 512,
-         "block_size": 32, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 512, "merge": "fused"},
-    ),
-    (
-        "b4-gqa32x8-c1024-d256-p16-fp16",
-        {"dtype": "fp16", "batch": 4, "query_heads": 32, "kv_heads": 8, "head_dim": 256, "num_blocks": 512,
-         "block_size": 16, "max_blocks_per_sequence": 64},
-        {"partition_tokens": 128, "merge": "fused"},
-    ),
+    (f"{case[0]}-{dtype}", _reference_region(case, dtype), REFERENCE_LAUNCH[case[0], dtype])
+    for case in REFERENCE_CASES for dtype in ("fp16", "bf16")
+] + [
     (
         "b128-gqa32x8-ragged-d128-p16-bf16",
         {"dtype": "bf16", "batch": 128, "query_heads": 32, "kv_heads": 8, "head_dim": 128,

@@ -25,7 +25,7 @@ from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint
 from radeon_kernels.runtime.pack import KernelPack
 from radeon_kernels.runtime.registry import DispatchManifest, DispatchRegistry
 from radeon_kernels.runtime.resources import builtin_contract, builtin_dispatch_registry
-from benchmarks.workloads import WORKLOADS
+from benchmarks.workloads import REFERENCE_KEYS, WORKLOADS
 from test_api import CaptureRuntime, FakeTensor, FakeTorch
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -75,6 +75,12 @@ EXPECTED = {
     "c4": ("paged_attention_decode-gfx950-b4-gqa32x8-c1024-d256-p16-fp16", 512, 64),
     "c5": ("paged_attention_decode-gfx950-b128-gqa32x8-ragged-d128-p16-bf16", 69713, 1024),
 }
+# The reference's eight workload cases in both dtypes, at the cache size its benchmark draws
+# (num_blocks = batch * max_blocks): each selects its own exact entry.
+EXPECTED.update({
+    key: (f"paged_attention_decode-gfx950-{key}", WORKLOADS[key].num_blocks, WORKLOADS[key].max_blocks)
+    for key in REFERENCE_KEYS
+})
 
 
 @pytest.mark.parametrize("key", sorted(EXPECTED))
@@ -89,6 +95,15 @@ def test_measured_workloads_select_their_exact_entry(key, index, scale):
     assert decision.entry_id == entry_id
     assert decision.winner.entrypoint == "decode_mfma"
     assert decision.launch["partition_tokens"] >= 16
+    assert decision.launch["merge"] in ("fused", "reduce")
+
+
+def test_every_reference_case_and_dtype_has_an_exact_entry():
+    """16 exact entries, one per (reference case, dtype), plus the 128-sequence ragged entry."""
+
+    ids = {suffix for suffix, _, _ in dispatch_plan.EXACT_REGIONS}
+    assert ids == set(REFERENCE_KEYS) | {"b128-gqa32x8-ragged-d128-p16-bf16"}
+    assert len(REFERENCE_KEYS) == 16
 
 
 def test_other_gfx950_shapes_use_broad_region_and_unsupported_ones_fall_back():

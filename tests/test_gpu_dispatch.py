@@ -188,3 +188,40 @@ def test_fused_calls_on_two_streams_use_separate_counters(gpu):
     torch.cuda.synchronize()
     for i in range(2):
         assert all(torch.equal(r, expected[i]) for r in results[i]), f"stream {i}"
+
+
+# ---------------------------------------------------------------------------------------------
+# The reference's eight workload cases in both dtypes (benchmarks/workloads/paged_attention_decode-1.0.yaml:
+# 13-22), drawn as its benchmark draws them, on its three seeds: each selects its exact gfx950 entry
+# through the public operator and matches the float64 oracle; the entry's launch in the other merge
+# form gives the same bits.
+def _reference_keys():
+    from benchmarks.workloads import REFERENCE_KEYS
+
+    return list(REFERENCE_KEYS)
+
+
+@pytest.mark.parametrize("key", _reference_keys())
+def test_reference_case_selects_its_entry_and_matches_oracle(gpu, palib, key):
+    import torch
+
+    import radeon_kernels as rk
+    from benchmarks.workloads import REFERENCE_SEEDS, WORKLOADS, make_inputs
+
+    w = WORKLOADS[key]
+    for seed in REFERENCE_SEEDS:
+        data = make_inputs(key, seed=seed)
+        dev = to_device(data, gpu)
+        announce(f"rk.paged_attention_decode reference case {key} seed {seed}")
+        args = (dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"], dev["context_lengths"])
+        out = rk.paged_attention_decode(*args)
+        record = rk.get_last_dispatch()
+        assert record["selected"] == "native/decode_mfma", rk.explain_last_dispatch()
+        assert record["entry_id"] == f"paged_attention_decode-gfx950-{key}"
+        assert_within(out, oracle64(data), w.dtype, f"{key} seed {seed}")
+        partition = record["launch"]["partition_tokens"]
+        fused = palib.decode(*args, partition_tokens=partition, phase="fused")
+        two = palib.decode(*args, partition_tokens=partition)
+        torch.cuda.synchronize()
+        assert torch.equal(fused.view(torch.int16), out.view(torch.int16))
+        assert torch.equal(two.view(torch.int16), out.view(torch.int16))

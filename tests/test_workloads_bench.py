@@ -82,17 +82,19 @@ def test_bench_reads_traffic_only_for_its_exact_configuration(tmp_path, monkeypa
 
     summary = tmp_path / "traffic.txt"
     summary.write_text("# measured\nworkload = b128-x\nvariant = mfma\npartition_tokens = 2048\n"
-                       "hbm_bytes_per_launch = 4867000000\n")
+                       "kv_bytes_per_call = 4237918208\nhbm_bytes_per_launch = 4867000000\n")
     monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", summary)
-    assert bench.read_traffic("b128-x", "mfma", 2048) == 4_867_000_000
-    assert bench.read_traffic("b128-x", "mfma", 1024) is None
-    assert bench.read_traffic("other", "mfma", 2048) is None
-    assert bench.read_traffic("b128-x", "mfma", 2048, "fused") is None  # measured in the reduce form
+    kv = 4_237_918_208
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv) == 4_867_000_000
+    assert bench.read_traffic("b128-x", "mfma", 1024, "reduce", kv) is None
+    assert bench.read_traffic("other", "mfma", 2048, "reduce", kv) is None
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv + 1) is None  # another input draw
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", kv) is None  # measured in the reduce form
     summary.write_text(summary.read_text() + "merge = fused\n")
-    assert bench.read_traffic("b128-x", "mfma", 2048, "fused") == 4_867_000_000
-    assert bench.read_traffic("b128-x", "mfma", 2048) is None
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", kv) == 4_867_000_000
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv) is None
     monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", tmp_path / "absent.txt")
-    assert bench.read_traffic("b128-x", "mfma", 2048) is None
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv) is None
 
 
 def test_case_traffic_matches_operator_case_and_dtype(tmp_path):
@@ -116,14 +118,44 @@ def test_committed_case_summaries_name_their_bench_workloads():
                                    "kv_cache_copy-beam-pairs64-gqa8-d256-p16-bf16") == 16_839_687
 
 
-def test_bench_uses_the_dispatch_table_launch():
+def test_bench_accepts_every_workload_and_defaults_to_b128():
     import bench
-    from radeon_kernels import dispatch_plan
 
-    entrypoint, partition, merge = bench.dispatch_launch("c5")
-    assert entrypoint == dispatch_plan.ENTRYPOINT
-    assert {"partition_tokens": partition, "merge": merge} == [
-        launch for suffix, _, launch in dispatch_plan.EXACT_REGIONS if suffix.startswith("b128")][0]
-    assert [bench.dispatch_launch(key)[2] for key in ("c1", "c2", "c3", "c4", "c5")] == ["fused"] * 4 + ["reduce"]
     args = bench.parse_args([])
     assert (args.gpus, args.workload) == (1, "c5")
+    for key in WORKLOADS:
+        assert bench.parse_args(["--workload", key]).workload == key
+
+
+def test_cpu_baseline_thread_count_respects_affinity_and_share(monkeypatch):
+    import bench
+
+    monkeypatch.setattr(bench.os, "sched_getaffinity", lambda pid: set(range(64)))
+    monkeypatch.setenv("OMP_NUM_THREADS", "16")
+    assert bench.cpu_threads() == (16, 64)
+    monkeypatch.delenv("OMP_NUM_THREADS")
+    assert bench.cpu_threads() == (64, 64)
+    monkeypatch.setattr(bench.os, "sched_getaffinity", lambda pid: set(range(8)))
+    monkeypatch.setenv("OMP_NUM_THREADS", "16")
+    assert bench.cpu_threads() == (8, 8)
+
+
+def test_cpu_baseline_protocol_on_a_small_workload():
+    """The CPU leg on CPU tensors: one warmup pass, at least three timed passes, the thread count set
+    and recorded with torch's parallel_info."""
+
+    import torch
+
+    import bench
+    from benchmarks.workloads import make_inputs
+
+    data = make_inputs("b1-gqa32x8-c128-d128-p16-fp16")
+    before = torch.get_num_threads()
+    try:
+        result = bench.cpu_baseline(torch, data, seconds=0.5)
+        assert result["cores"] == bench.cpu_threads()[0] == torch.get_num_threads()
+    finally:
+        torch.set_num_threads(before)
+    assert 3 <= result["pass_seconds"]["passes"] <= 30 and result["value"] > 0
+    assert result["kind"] == "port" and "1 warmup pass" in result["sample"]
+    assert any("ATen" in line or "OpenMP" in line for line in result["parallel_info"])

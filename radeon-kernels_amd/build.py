@@ -255,7 +255,21 @@ def write_pack_and_dispatch(bindings: dict[str, Path]) -> dict:
     return {"sha256": digests, "environment": environment, "entries": entries}
 
 
+def compile_launch_loops(verbose: bool = False) -> Path:
+    """The promotion timing's C launch loops (promotion/launch_loop.c): plain C, no GPU code."""
+
+    source = PACKAGE_ROOT / "promotion" / "launch_loop.c"
+    target = PACKAGE_ROOT / "promotion" / "liblaunch_loop.so"
+    temporary = PACKAGE_ROOT / "_build" / "liblaunch_loop.so"
+    temporary.parent.mkdir(exist_ok=True)
+    _finish(_run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-Werror", f"-ffile-prefix-map={REPO_ROOT}=.",
+                  str(source), "-Wl,--build-id=none", "-o", str(temporary)], verbose), "gcc (launch_loop.c)")
+    os.replace(temporary, target)
+    return target
+
+
 def build(verbose: bool = False) -> dict:
+    compile_launch_loops(verbose)
     summary = write_pack_and_dispatch(compile_libraries(verbose=verbose))
     # Sign the pack manifest (the runtime loads only signed packs) and rewrite the promotion records
     # from the committed GPU evaluations (promotion/publish.py).

@@ -11,10 +11,12 @@ and all in the reference's formats:
 * ``proposals/<proposal_id>.json`` -- the deterministic gates of
   developer/promotion/create_operator_proposal.py:87-237 (artifact and environment consistency,
   correctness, CV <= 3%, latency reduction and the lower end of its 95% paired-bootstrap interval
-  >= 3% against the torch fallback), plus one gate of this build: every exact gfx950 dispatch entry
-  of the operator has correctness cases;
+  >= 3% against the torch fallback) on the headline entry, and the same timing gates on every exact
+  gfx950 dispatch entry of the operator, each of which must also have correctness cases;
 * for a proposal whose gates all pass: ``approvals/<approval_id>.json`` (schemas/approval.schema.json),
-  ``evidence/<evidence_id>.json`` (schemas/evidence.schema.json) and
+  ``evidence/<evidence_id>.json`` (schemas/evidence.schema.json; the pack-level record, timed on the
+  headline entry), one ``evidence/<evidence_id>.<entry>.json`` per exact entry (that entry's
+  workload, correctness cases and timing, as the reference publishes one record per winner) and
   ``pack-index/<operator>-1.0.json`` (schemas/pack-index.schema.json), each with its ``.sig.json``;
 * ``releases/<pack_id>-<pack_version>.tar.gz`` -- the release archive the pack-index record names:
   exactly the manifest, its signature and the artifacts the manifest lists (the payload the
@@ -29,9 +31,9 @@ What differs from the reference's flow, deliberately:
   created once by ``publish.py --create-release-key``).  A machine without it signs with its own
   development key, trusted only by a process that names ``.signing/dev-trusted-keys.json`` in
   RADEON_KERNELS_DEV_TRUSTED_KEYS; this tool never writes the built-in keyring after set-up;
-* one pack holds all three operators, so each operator has one evidence record covering all of its
-  exact dispatch entries (correctness cases for each, timing on the headline workload), where the
-  reference builds one pack and one evidence record per workload.
+* one pack holds all four operators, so the pack names one evidence id per operator (the record
+  timed on the headline entry) and the per-entry records sit beside it under the same approval,
+  where the reference builds one pack and one evidence record per workload.
 
 Records of a proposal that no longer passes (for example after a kernel change, until the GPU
 evaluation is rerun) are removed, so the tree never shows evidence for artifacts it does not hold.
@@ -226,6 +228,38 @@ def _scalar_workload(constraints: dict[str, Any]) -> dict[str, Any]:
     return out
 
 
+def timing_summary(timing: dict[str, Any], baseline_name: str) -> dict[str, Any]:
+    """The evidence schema's timing object from one paired timing record of an evaluation."""
+
+    candidate = [float(v) for v in timing["candidate"]["samples_ms"]]
+    baseline = [float(v) for v in timing["baseline"]["samples_ms"]]
+    interval = bootstrap_interval(candidate, baseline)
+    candidate_cv = float(timing["candidate"]["coefficient_of_variation"])
+    baseline_cv = float(timing["baseline"]["coefficient_of_variation"])
+    return {
+        "baseline": baseline_name,
+        "candidate_samples_ms": candidate,
+        "baseline_samples_ms": baseline,
+        "candidate_median_ms": float(timing["candidate"]["median_ms"]),
+        "baseline_median_ms": float(timing["baseline"]["median_ms"]),
+        "candidate_cv": candidate_cv,
+        "baseline_cv": baseline_cv,
+        "latency_reduction_pct": latency_reduction(candidate, baseline),
+        "confidence_interval_pct": list(interval),
+        "stable": candidate_cv <= MAXIMUM_CV and baseline_cv <= MAXIMUM_CV,
+    }
+
+
+def public_case(case: dict[str, Any]) -> dict[str, Any]:
+    """A correctness case in the evidence schema's fields (guards_intact where it was checked)."""
+
+    out = {"case_id": case["case_id"], "seed": int(case["seed"]), "runtime_ok": bool(case["runtime_ok"]),
+           "finite": bool(case["finite"]), "max_absolute_error": float(case["max_absolute_error"])}
+    if "guards_intact" in case:
+        out["guards_intact"] = bool(case["guards_intact"])
+    return out
+
+
 def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
     from radeon_kernels.runtime.pack import KernelPack
     from radeon_kernels.runtime.registry import DispatchManifest
@@ -247,6 +281,9 @@ def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
     baseline = [float(v) for v in timing["baseline"]["samples_ms"]]
     reduction = latency_reduction(candidate, baseline)
     interval = bootstrap_interval(candidate, baseline)
+    per_entry = {entry_id: timing_summary(record["timing"], record["timing"].get("baseline_method",
+                                                                                  evaluation["baseline"]))
+                 for entry_id, record in evaluation.get("entries", {}).items()}
     env = evaluation["environment"]
     pack_env = pack.environment
     gates = {
@@ -262,6 +299,13 @@ def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
         "baseline_stable": timing["baseline"]["coefficient_of_variation"] <= MAXIMUM_CV,
         "improvement_threshold_passed": reduction >= MINIMUM_IMPROVEMENT_PCT,
         "confidence_threshold_passed": interval[0] >= MINIMUM_IMPROVEMENT_PCT,
+        "every_exact_entry_timed": exact_ids <= set(per_entry),
+        "graph_replays_match_eager": all(record["timing"].get("graph_replay_matches_eager", True)
+                                         for record in evaluation.get("entries", {}).values()),
+        "every_entry_stable": bool(per_entry) and all(t["stable"] for t in per_entry.values()),
+        "every_entry_improved": bool(per_entry) and all(
+            t["latency_reduction_pct"] >= MINIMUM_IMPROVEMENT_PCT
+            and t["confidence_interval_pct"][0] >= MINIMUM_IMPROVEMENT_PCT for t in per_entry.values()),
     }
     failed = [name for name, passed in gates.items() if not passed]
     decision = "promote" if not failed else "needs_review"
@@ -272,6 +316,7 @@ def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
         "manifest": _sha256((PACK_DIR / "manifest.json").read_bytes()),
     }
     environment = {k: v for k, v in pack_env.to_dict().items() if k != "features"}
+    case_entry = {case["case_id"]: case["entry_id"] for case in evaluation["cases"]}
     workload = _scalar_workload(headline_entry["workload"])
     workload["evidence_scope"] = (f"all {len(exact_ids)} exact gfx950 entries (correctness); "
                                   f"timing on {evaluation['headline_entry_id']}")
@@ -287,22 +332,9 @@ def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
         "correctness": {
             "passed": gates["correctness_passed"],
             "oracle": evaluation["oracle"],
-            "cases": [{"case_id": case["case_id"], "seed": int(case["seed"]), "runtime_ok": bool(case["runtime_ok"]),
-                       "finite": bool(case["finite"]), "max_absolute_error": float(case["max_absolute_error"])}
-                      for case in evaluation["cases"]],
+            "cases": [public_case(case) for case in evaluation["cases"]],
         },
-        "timing": {
-            "baseline": evaluation["baseline"],
-            "candidate_samples_ms": candidate,
-            "baseline_samples_ms": baseline,
-            "candidate_median_ms": float(timing["candidate"]["median_ms"]),
-            "baseline_median_ms": float(timing["baseline"]["median_ms"]),
-            "candidate_cv": float(timing["candidate"]["coefficient_of_variation"]),
-            "baseline_cv": float(timing["baseline"]["coefficient_of_variation"]),
-            "latency_reduction_pct": reduction,
-            "confidence_interval_pct": list(interval),
-            "stable": gates["candidate_stable"] and gates["baseline_stable"],
-        },
+        "timing": timing_summary(timing, evaluation["baseline"]),
         "source_evidence_hashes": sources,
         "decision": decision,
         "guarantee_boundary": (
@@ -310,6 +342,25 @@ def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
             f"{pack_env.pytorch_version}; the exact gfx950 dispatch entries "
             f"{', '.join(sorted(exact_ids))}; contiguous inference only."),
     }
+    # One evidence record per exact entry, as the reference publishes one per winner: that entry's
+    # workload, correctness cases and paired timing.
+    raw_entries = {raw["id"]: raw for raw in dispatch_raw["entries"]}
+    prefix = f"{operator}-gfx950-"
+    entry_evidence = []
+    for entry_id in sorted(exact_ids & set(per_entry)):
+        entry_cases = [case for case in public_evidence["correctness"]["cases"]
+                       if case_entry.get(case["case_id"]) == entry_id]
+        entry_evidence.append({
+            **public_evidence,
+            "evidence_id": f"{item.evidence_id}.{entry_id[len(prefix):]}",
+            "workload": _scalar_workload(raw_entries[entry_id]["workload"]),
+            "correctness": {"passed": all(c["passed"] for c in evaluation["cases"] if c["entry_id"] == entry_id),
+                            "oracle": evaluation["oracle"], "cases": entry_cases},
+            "timing": per_entry[entry_id],
+            "guarantee_boundary": (
+                f"Exact {pack_env.architecture}, ROCm {pack_env.rocm_abi}, {pack_env.python_abi}, PyTorch "
+                f"{pack_env.pytorch_version}; the gfx950 dispatch entry {entry_id}; contiguous inference only."),
+        })
     identity = _sha256(json.dumps({"evidence_id": item.evidence_id, "sources": sources},
                                   sort_keys=True).encode())[:16]
     return {
@@ -328,6 +379,7 @@ def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
         "recommended_decision": decision,
         "reasons": ["all deterministic promotion gates passed"] if not failed else failed,
         "public_evidence": public_evidence,
+        "entry_evidence": entry_evidence,
     }
 
 
@@ -412,9 +464,11 @@ def publish(verbose: bool = False) -> dict[str, str]:
                 "approval_id": approval_id,
             }],
         }
-        for directory, name, document in (("approvals", approval_id, approval),
-                                          ("evidence", evidence["evidence_id"], evidence),
-                                          ("pack-index", f"{operator}-1.0", index)):
+        documents = [("approvals", approval_id, approval), ("evidence", evidence["evidence_id"], evidence),
+                     ("pack-index", f"{operator}-1.0", index)]
+        documents += [("evidence", record["evidence_id"], dict(record, approval_id=approval_id))
+                      for record in proposal["entry_evidence"]]
+        for directory, name, document in documents:
             path = RECORD_DIRS[directory] / f"{name}.json"
             _write(path, _json_bytes(document))
             keep.update({path, sign(path, key_id, key)})

@@ -5,8 +5,10 @@ matched or not, is written to the explain record (the operator runtime, which re
 outcome of each call itself, asks for no intermediate record).  No search, tuning or compilation
 happens here: an unmatched request gets the manifest's declared fallbacks.
 
-Manifests are immutable once loaded, so a decision depends only on (operator, version, fingerprint,
-signature); decisions are memoised on that key (the reference rescans every entry per call).
+Manifests are immutable once loaded and compiled into per-environment groups in priority order
+(runtime/registry.py), so a decision walks only the caller's group and depends only on (operator,
+version, fingerprint, signature); decisions are memoised on that key (the reference rescans every
+entry per call).
 """
 
 from __future__ import annotations
@@ -87,13 +89,7 @@ class Dispatcher:
 
     def _decide(self, request: DispatchRequest, fingerprint: EnvironmentFingerprint) -> DispatchDecision:
         manifest = self._registry.get(request.operator, request.semantic_version)
-        best = None
-        for entry in manifest.entries:
-            if entry.matches(fingerprint, request.signature):
-                # Overlapping entries always differ in priority (validated at load), so the
-                # maximum is unique.
-                if best is None or entry.priority > best.priority:
-                    best = entry
+        best = manifest.select(fingerprint, request.signature)
         if best is None:
             decision = DispatchDecision(
                 operator=request.operator,

@@ -1,9 +1,15 @@
 """Identity of the executing ROCm environment.
 
-Interface of src/radeon_kernels/runtime/fingerprint.py:37-128 in the reference: a dispatch entry
-only matches a process whose GPU architecture, wavefront size, ROCm ABI (MAJOR.MINOR), CPython ABI
-tag and exact PyTorch build string equal the entry's.  On MI355X the architecture is ``gfx950`` and
-the wavefront size is 64.
+Reference interface: src/radeon_kernels/runtime/fingerprint.py:37-128.  A dispatch entry or a kernel
+pack applies to a process only when five identity fields are equal -- GPU architecture, wavefront
+size, ROCm ABI (MAJOR.MINOR), CPython ABI tag and the exact PyTorch build string -- while
+architecture features only narrow.  On MI355X the architecture is ``gfx950`` and the wavefront 64.
+
+The five fields are defined once, as ``EnvironmentKey`` and the rule table ``_RULES`` (one checker
+per field, each returning the normalised value or naming what it expected).  The fingerprint (what
+this process is) and the environment constraint of manifests and packs (runtime/compatibility.py)
+both build their key through that table, so they accept exactly the same values, and environment
+matching is an equality of keys plus a feature-set inclusion.
 """
 
 from __future__ import annotations
@@ -11,37 +17,103 @@ from __future__ import annotations
 import re
 import sys
 from dataclasses import dataclass
-from typing import Any, Iterable, Mapping
+from typing import Any, Callable, Iterable, Mapping, NamedTuple
 
 from radeon_kernels.errors import RadeonKernelsError
-
-_ARCH = re.compile(r"gfx[0-9a-f]+")
-_ROCM = re.compile(r"(\d+)\.(\d+)")
-_PY_ABI = re.compile(r"cp\d{2,3}")
-_FIELDS = ("architecture", "wavefront_size", "rocm_abi", "python_abi", "pytorch_version", "features")
 
 
 class FingerprintError(RadeonKernelsError):
     """The local ROCm environment cannot be identified safely."""
 
 
+class IdentityValueError(ValueError):
+    """One identity value is invalid; the message says what was expected."""
+
+
+def _architecture(value: Any) -> str:
+    if isinstance(value, str) and re.fullmatch(r"gfx[0-9a-f]+", value):
+        return value
+    raise IdentityValueError("expected a gfx architecture")
+
+
+def _wavefront(value: Any) -> int:
+    if type(value) is int and value in (32, 64):
+        return value
+    raise IdentityValueError("expected 32 or 64")
+
+
+def _rocm(value: Any) -> str:
+    # "7.0.51831" -> "7.0" and "7.02.51831-rc1" -> "7.2": the ABI is the numeric major.minor prefix.
+    found = re.match(r"(\d+)\.(\d+)", value.strip()) if isinstance(value, str) else None
+    if found is None:
+        raise IdentityValueError("expected MAJOR.MINOR")
+    return f"{int(found[1])}.{int(found[2])}"
+
+
+def _python_abi(value: Any) -> str:
+    if isinstance(value, str) and re.fullmatch(r"cp\d{2,3}", value):
+        return value
+    raise IdentityValueError("expected a cpXY ABI tag")
+
+
+def _pytorch(value: Any) -> str:
+    if isinstance(value, str) and value:
+        return value
+    raise IdentityValueError("expected an exact build version")
+
+
+_RULES: dict[str, Callable[[Any], Any]] = {
+    "architecture": _architecture,
+    "wavefront_size": _wavefront,
+    "rocm_abi": _rocm,
+    "python_abi": _python_abi,
+    "pytorch_version": _pytorch,
+}
+
+
+def checked_features(values: Iterable[Any]) -> frozenset[str]:
+    """Feature names: non-empty words of letters, digits and underscores."""
+
+    features = frozenset(values)
+    for item in features:
+        if not (isinstance(item, str) and re.fullmatch(r"\w+", item, flags=re.ASCII)):
+            raise IdentityValueError("contains an invalid feature")
+    return features
+
+
+class EnvironmentKey(NamedTuple):
+    """The five exact-match identity fields, normalised."""
+
+    architecture: str
+    wavefront_size: int
+    rocm_abi: str
+    python_abi: str
+    pytorch_version: str
+
+    @classmethod
+    def checked(cls, raw: Mapping[str, Any], failure: Callable[[str, str], Exception]) -> EnvironmentKey:
+        """The key of ``raw``; an invalid field raises ``failure(field, expectation)``."""
+
+        values = []
+        for name, rule in _RULES.items():
+            try:
+                values.append(rule(raw[name]))
+            except IdentityValueError as problem:
+                raise failure(name, str(problem)) from None
+        return cls(*values)
+
+
 def normalize_rocm_abi(value: str) -> str:
     """``"7.0.51831"`` -> ``"7.0"``; leading zeros dropped; anything else is rejected."""
 
-    found = _ROCM.match(value.strip())
-    if found is None:
-        raise FingerprintError(f"invalid ROCm version: {value!r}")
-    major, minor = (int(part) for part in found.groups())
-    return f"{major}.{minor}"
+    try:
+        return _rocm(value)
+    except IdentityValueError as problem:
+        raise FingerprintError(f"invalid ROCm version {value!r} ({problem})") from None
 
 
-def _normalized_features(values: Iterable[str]) -> tuple[str, ...]:
-    seen: set[str] = set()
-    for item in values:
-        if not isinstance(item, str) or not item or not item.replace("_", "").isalnum():
-            raise FingerprintError(f"invalid architecture feature: {item!r}")
-        seen.add(item)
-    return tuple(sorted(seen))
+def _fingerprint_failure(name: str, problem: str) -> FingerprintError:
+    return FingerprintError(f"invalid {name.replace('_', ' ')} ({problem})")
 
 
 @dataclass(frozen=True)
@@ -54,36 +126,36 @@ class EnvironmentFingerprint:
     features: tuple[str, ...] = ()
 
     def __post_init__(self) -> None:
-        if not isinstance(self.architecture, str) or _ARCH.fullmatch(self.architecture) is None:
-            raise FingerprintError(f"invalid AMDGPU architecture: {self.architecture!r}")
-        if isinstance(self.wavefront_size, bool) or self.wavefront_size not in (32, 64):
-            raise FingerprintError("wavefront size must be 32 or 64")
-        object.__setattr__(self, "rocm_abi", normalize_rocm_abi(self.rocm_abi))
-        if not isinstance(self.python_abi, str) or _PY_ABI.fullmatch(self.python_abi) is None:
-            raise FingerprintError("Python ABI must use the cpXY form")
-        if not self.pytorch_version:
-            raise FingerprintError("PyTorch version must not be empty")
-        object.__setattr__(self, "features", _normalized_features(self.features))
+        key = EnvironmentKey.checked({name: getattr(self, name) for name in EnvironmentKey._fields},
+                                     _fingerprint_failure)
+        for name, value in key._asdict().items():
+            object.__setattr__(self, name, value)
+        if isinstance(self.features, (str, bytes)):
+            raise FingerprintError("features must be a collection of names")
+        try:
+            features = checked_features(self.features)
+        except (IdentityValueError, TypeError) as problem:
+            raise FingerprintError(f"invalid architecture features ({problem})") from None
+        object.__setattr__(self, "features", tuple(sorted(features)))
+
+    @property
+    def key(self) -> EnvironmentKey:
+        return EnvironmentKey(self.architecture, self.wavefront_size, self.rocm_abi, self.python_abi,
+                              self.pytorch_version)
 
     @classmethod
     def from_mapping(cls, value: Mapping[str, Any]) -> EnvironmentFingerprint:
-        extra = sorted(set(value) - set(_FIELDS))
+        known = set(EnvironmentKey._fields) | {"features"}
+        extra = sorted(set(value) - known)
         if extra:
             raise FingerprintError(f"unknown fingerprint fields: {extra}")
-        features = value.get("features", ())
-        if isinstance(features, (str, bytes)):
+        if not set(EnvironmentKey._fields) <= set(value) or isinstance(value.get("features"), (str, bytes)):
             raise FingerprintError("fingerprint has missing or invalid fields")
         try:
-            return cls(
-                architecture=value["architecture"],
-                wavefront_size=value["wavefront_size"],
-                rocm_abi=value["rocm_abi"],
-                python_abi=value["python_abi"],
-                pytorch_version=value["pytorch_version"],
-                features=tuple(features),
-            )
-        except (KeyError, TypeError, AttributeError) as error:
+            features = tuple(value.get("features", ()))
+        except TypeError as error:
             raise FingerprintError("fingerprint has missing or invalid fields") from error
+        return cls(**{name: value[name] for name in EnvironmentKey._fields}, features=features)
 
     @classmethod
     def detect(
@@ -94,40 +166,28 @@ class EnvironmentFingerprint:
         features: Iterable[str] = (),
         python_abi: str | None = None,
     ) -> EnvironmentFingerprint:
-        """Read the fingerprint of ``device_index`` from PyTorch (imported lazily)."""
+        """The fingerprint of GPU ``device_index`` as PyTorch reports it (PyTorch imported lazily)."""
 
-        if torch_module is None:
+        torch = torch_module
+        if torch is None:
             try:
-                import torch as torch_module
+                import torch
             except ImportError as error:
-                raise FingerprintError(
-                    "PyTorch is required to detect the ROCm environment"
-                ) from error
-        if not torch_module.cuda.is_available():
+                raise FingerprintError("PyTorch is required to detect the ROCm environment") from error
+        if not torch.cuda.is_available():
             raise FingerprintError("no visible ROCm GPU")
-        hip_version = getattr(torch_module.version, "hip", None)
-        if not isinstance(hip_version, str) or not hip_version:
+        hip = getattr(torch.version, "hip", None)
+        if not (isinstance(hip, str) and hip):
             raise FingerprintError("the installed PyTorch build does not report a ROCm version")
-        properties = torch_module.cuda.get_device_properties(device_index)
-        architecture = str(getattr(properties, "gcnArchName", "")).split(":", 1)[0]
-        wavefront = getattr(properties, "warp_size", None)
-        if isinstance(wavefront, bool) or not isinstance(wavefront, int):
+        device = torch.cuda.get_device_properties(device_index)
+        wavefront = getattr(device, "warp_size", None)
+        if type(wavefront) is not int:
             raise FingerprintError("PyTorch did not report the GPU wavefront size")
-        return cls(
-            architecture=architecture,
-            wavefront_size=wavefront,
-            rocm_abi=hip_version,
-            python_abi=python_abi or f"cp{sys.version_info.major}{sys.version_info.minor}",
-            pytorch_version=str(torch_module.__version__),
-            features=tuple(features),
-        )
+        # gcnArchName carries target features after the name: "gfx950:sramecc+:xnack-".
+        architecture = str(getattr(device, "gcnArchName", "")).partition(":")[0]
+        return cls(architecture=architecture, wavefront_size=wavefront, rocm_abi=hip,
+                   python_abi=python_abi or "cp{}{}".format(*sys.version_info[:2]),
+                   pytorch_version=str(torch.__version__), features=tuple(features))
 
     def to_dict(self) -> dict[str, Any]:
-        return {
-            "architecture": self.architecture,
-            "wavefront_size": self.wavefront_size,
-            "rocm_abi": self.rocm_abi,
-            "python_abi": self.python_abi,
-            "pytorch_version": self.pytorch_version,
-            "features": list(self.features),
-        }
+        return {**self.key._asdict(), "features": list(self.features)}

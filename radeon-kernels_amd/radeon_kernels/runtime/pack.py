@@ -1,37 +1,37 @@
 """Kernel-pack manifests (``<pack>/manifest.json``).
 
-Document format of the reference's schemas/kernel-pack.schema.json and rules of
-src/radeon_kernels/runtime/pack.py:35-157: a pack binds one exact environment to a list of
-artifacts, each tagged with operator, semantic version, provider, relative path, entrypoint,
-SHA-256, format and evidence id; (operator, semantic_version) pairs and artifact paths are unique
-within a pack.
+Document format of the reference's schemas/kernel-pack.schema.json, rules of
+src/radeon_kernels/runtime/pack.py:35-157: a pack binds one environment constraint to a non-empty
+list of artifacts.  An artifact record is a dispatch winner (provider, relative path, entrypoint,
+SHA-256, format -- every field required here) tagged with the operator, semantic version and
+evidence id it serves.  Within a pack, (operator, semantic version) pairs and artifact paths are
+unique; the pack is indexed by the former, which is how the runtime looks artifacts up.
 """
 
 from __future__ import annotations
 
 import json
-import re
-from dataclasses import dataclass
+from dataclasses import dataclass, field, replace
 from pathlib import Path
+from types import MappingProxyType
 from typing import Any, Mapping
 
 from radeon_kernels.errors import ConfigError
+from radeon_kernels.runtime import fields
 from radeon_kernels.runtime.compatibility import EnvironmentConstraint
 from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint
 from radeon_kernels.runtime.loader import PrecompiledArtifactLoader
-from radeon_kernels.runtime.registry import ArtifactSpec, identifier, require_fields
+from radeon_kernels.runtime.registry import ARTIFACT_FIELDS, ArtifactSpec
 
-_VERSION = re.compile(r"\d+\.\d+")
-_PACK_VERSION = re.compile(r"\d+\.\d+\.\d+")
 SUPPORTED_SCHEMA_VERSION = "1.0"
-_ARTIFACT_FIELDS = ("operator", "semantic_version", "provider", "artifact", "entrypoint", "sha256", "format", "evidence_id")
-_PACK_FIELDS = ("schema_version", "pack_id", "pack_version", "environment", "artifacts")
 
-
-def _checked_version(value: Any, path: str, pattern: re.Pattern[str]) -> str:
-    if isinstance(value, str) and pattern.fullmatch(value):
-        return value
-    raise ConfigError(path, "invalid version")
+_SPEC_NAMES = tuple(spec.name for spec in ARTIFACT_FIELDS)
+_ARTIFACT_RECORD = (
+    fields.Field("operator", fields.identifier),
+    fields.Field("semantic_version", fields.major_minor),
+    *(replace(spec, required=True) for spec in ARTIFACT_FIELDS),
+    fields.Field("evidence_id", fields.identifier),
+)
 
 
 @dataclass(frozen=True)
@@ -43,24 +43,40 @@ class KernelPackArtifact:
 
     @classmethod
     def from_mapping(cls, value: Any, path: str) -> KernelPackArtifact:
-        if not isinstance(value, Mapping):
-            raise ConfigError(path, "expected a mapping")
-        require_fields(value, _ARTIFACT_FIELDS, _ARTIFACT_FIELDS, path)
-        spec = ArtifactSpec.from_mapping(
-            {key: value[key] for key in ("provider", "artifact", "entrypoint", "sha256", "format")}, path
-        )
-        return cls(
-            operator=identifier(value["operator"], f"{path}.operator"),
-            semantic_version=_checked_version(value["semantic_version"], f"{path}.semantic_version", _VERSION),
-            artifact=spec,
-            evidence_id=identifier(value["evidence_id"], f"{path}.evidence_id"),
-        )
+        record = fields.read_record(value, _ARTIFACT_RECORD, path)
+        spec = ArtifactSpec(**{name: record.pop(name) for name in _SPEC_NAMES})
+        return cls(artifact=spec, **record)
 
     def to_dict(self) -> dict[str, Any]:
-        record = {"operator": self.operator, "semantic_version": self.semantic_version}
-        record.update(self.artifact.to_dict())
-        record["evidence_id"] = self.evidence_id
-        return record
+        return {"operator": self.operator, "semantic_version": self.semantic_version, **self.artifact.to_dict(),
+                "evidence_id": self.evidence_id}
+
+
+def _schema_version(value: Any, path: str) -> str:
+    version = fields.major_minor(value, path)
+    if version != SUPPORTED_SCHEMA_VERSION:
+        raise ConfigError(path, f"unsupported version {version!r}")
+    return version
+
+
+def _artifact_list(value: Any, path: str) -> tuple[KernelPackArtifact, ...]:
+    if not isinstance(value, list) or not value:
+        raise ConfigError(path, "expected a non-empty list")
+    items = tuple(KernelPackArtifact.from_mapping(item, f"{path}[{index}]") for index, item in enumerate(value))
+    if len({(item.operator, item.semantic_version) for item in items}) != len(items):
+        raise ConfigError(path, "operator semantic versions must be unique")
+    if len({item.artifact.artifact for item in items}) != len(items):
+        raise ConfigError(path, "artifact paths must be unique")
+    return items
+
+
+_PACK_RECORD = (
+    fields.Field("schema_version", _schema_version),
+    fields.Field("pack_id", fields.identifier),
+    fields.Field("pack_version", fields.pack_version),
+    fields.Field("environment", EnvironmentConstraint.from_mapping),
+    fields.Field("artifacts", _artifact_list),
+)
 
 
 @dataclass(frozen=True)
@@ -71,6 +87,12 @@ class KernelPack:
     pack_version: str
     environment: EnvironmentConstraint
     artifacts: tuple[KernelPackArtifact, ...]
+    _by_operator: Mapping[tuple[str, str], KernelPackArtifact] = field(
+        init=False, compare=False, repr=False, hash=False)
+
+    def __post_init__(self) -> None:
+        index = {(item.operator, item.semantic_version): item for item in self.artifacts}
+        object.__setattr__(self, "_by_operator", MappingProxyType(index))
 
     @classmethod
     def from_directory(cls, root: Path, *, verify_artifacts: bool = True) -> KernelPack:
@@ -78,40 +100,14 @@ class KernelPack:
             resolved = Path(root).resolve(strict=True)
         except OSError as error:
             raise ConfigError(str(root), "kernel pack directory does not exist") from error
-        manifest_path = resolved / "manifest.json"
+        manifest = resolved / "manifest.json"
         try:
-            document = json.loads(manifest_path.read_text(encoding="utf-8"))
+            document = json.loads(manifest.read_text(encoding="utf-8"))
         except OSError as error:
-            raise ConfigError(str(manifest_path), str(error)) from error
+            raise ConfigError(str(manifest), str(error)) from error
         except json.JSONDecodeError as error:
-            raise ConfigError(str(manifest_path), f"invalid JSON: {error.msg}") from error
-        path = str(manifest_path)
-        if not isinstance(document, Mapping):
-            raise ConfigError(path, "expected a mapping")
-        require_fields(document, _PACK_FIELDS, _PACK_FIELDS, path)
-        schema_version = _checked_version(document["schema_version"], f"{path}.schema_version", _VERSION)
-        if schema_version != SUPPORTED_SCHEMA_VERSION:
-            raise ConfigError(f"{path}.schema_version", f"unsupported version {schema_version!r}")
-        raw_artifacts = document["artifacts"]
-        if not isinstance(raw_artifacts, list) or not raw_artifacts:
-            raise ConfigError(f"{path}.artifacts", "expected a non-empty list")
-        pack = cls(
-            root=resolved,
-            schema_version=schema_version,
-            pack_id=identifier(document["pack_id"], f"{path}.pack_id"),
-            pack_version=_checked_version(document["pack_version"], f"{path}.pack_version", _PACK_VERSION),
-            environment=EnvironmentConstraint.from_mapping(document["environment"], f"{path}.environment"),
-            artifacts=tuple(
-                KernelPackArtifact.from_mapping(item, f"{path}.artifacts[{index}]")
-                for index, item in enumerate(raw_artifacts)
-            ),
-        )
-        keys = [(item.operator, item.semantic_version) for item in pack.artifacts]
-        if len(set(keys)) != len(keys):
-            raise ConfigError(f"{path}.artifacts", "operator semantic versions must be unique")
-        paths = [item.artifact.artifact for item in pack.artifacts]
-        if len(set(paths)) != len(paths):
-            raise ConfigError(f"{path}.artifacts", "artifact paths must be unique")
+            raise ConfigError(str(manifest), f"invalid JSON: {error.msg}") from error
+        pack = cls(root=resolved, **fields.read_record(document, _PACK_RECORD, str(manifest)))
         if verify_artifacts:
             loader = PrecompiledArtifactLoader(pack.root)
             for item in pack.artifacts:
@@ -121,10 +117,12 @@ class KernelPack:
     def matches(self, fingerprint: EnvironmentFingerprint) -> bool:
         return self.environment.matches(fingerprint)
 
+    def find(self, operator: str, semantic_version: str) -> KernelPackArtifact | None:
+        return self._by_operator.get((operator, semantic_version))
+
     def get(self, operator: str, semantic_version: str) -> KernelPackArtifact:
-        for item in self.artifacts:
-            if item.operator == operator and item.semantic_version == semantic_version:
-                return item
-        raise ConfigError(
-            self.pack_id, f"pack has no artifact for {operator!r} semantic version {semantic_version!r}"
-        )
+        item = self.find(operator, semantic_version)
+        if item is None:
+            raise ConfigError(self.pack_id,
+                              f"pack has no artifact for {operator!r} semantic version {semantic_version!r}")
+        return item

@@ -1,20 +1,22 @@
 """Kernel-pack discovery and resolution.
 
-Interface of src/radeon_kernels/runtime/packs.py:20-147 in the reference: pack roots come from
-``RADEON_KERNELS_PACK_PATH`` (os.pathsep separated), the user data directory and the interpreter
-prefix; a root is either a pack itself (contains ``manifest.json``) or a directory of packs;
-invalid packs are collected as ``rejected`` rather than raised; ``resolve`` needs a pack whose
-environment matches the fingerprint and whose artifact record equals the dispatch winner exactly.
+Reference interface: src/radeon_kernels/runtime/packs.py:20-147.
 
-Signatures are required by default, as in the reference (packs.py:88-113): every pack's
-``manifest.json`` must carry a ``manifest.sig.json`` that verifies under the trusted keyring
-(radeon_kernels.runtime.signing; the built-in release keyring, plus the development keyring an
-opt-in environment variable names, unless a keyring is given), else the pack is
-rejected with the reason.
+Roots, in order: the ``RADEON_KERNELS_PACK_PATH`` entries (``os.pathsep`` separated), the user data
+directory, the interpreter prefix and, last, the in-tree pack directory the build writes
+(``radeon-kernels_amd/packs``) -- that one is this build's addition, so a source checkout finds its
+own gfx950 pack without installing it.  A root is a pack itself (it holds ``manifest.json``) or a
+directory of packs.
 
-One deliberate difference: the in-tree pack directory written by the build
-(``radeon-kernels_amd/packs``) is appended as the last default root, so a source checkout finds its
-own gfx950 pack without installation.  The build signs that pack's manifest with its development key.
+Discovery is total: a pack that cannot be read or verified is recorded in ``rejected`` with its
+reason, never raised.  Signatures are required by default (reference packs.py:88-113): a pack's
+``manifest.json`` must carry a ``manifest.sig.json`` that verifies under the trusted keyring (the
+built-in release keyring, plus the development keyring an opt-in environment variable names,
+unless a keyring is given).
+
+Accepted packs are indexed by (environment key, operator, semantic version).  Resolution looks up
+the caller's key and then needs a pack whose required features the fingerprint has and whose
+artifact record and evidence id equal the approved dispatch entry's exactly.
 """
 
 from __future__ import annotations
@@ -25,12 +27,11 @@ from dataclasses import dataclass
 from pathlib import Path
 from typing import Iterable, Mapping, Sequence
 
-from radeon_kernels.errors import ConfigError, RadeonKernelsError
-from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint
+from radeon_kernels.errors import RadeonKernelsError
+from radeon_kernels.runtime.fingerprint import EnvironmentFingerprint, EnvironmentKey
 from radeon_kernels.runtime.pack import KernelPack, KernelPackArtifact
 from radeon_kernels.runtime.registry import ArtifactSpec
 from radeon_kernels.runtime.signing import (
-    SignatureVerificationError,
     TrustedKeyring,
     default_trusted_keyring,
     verify_detached_file,
@@ -57,41 +58,38 @@ def default_pack_roots(
     prefix: Path | None = None,
     include_in_tree: bool = True,
 ) -> tuple[Path, ...]:
-    environment = os.environ if environ is None else environ
-    candidates = [Path(item).expanduser() for item in environment.get(PACK_PATH_ENVIRONMENT_VARIABLE, "").split(os.pathsep) if item]
-    candidates.append((home or Path.home()) / ".local" / "share" / "radeon-kernels" / "packs")
-    candidates.append((prefix or Path(sys.prefix)) / "share" / "radeon-kernels" / "packs")
+    listed = (os.environ if environ is None else environ).get(PACK_PATH_ENVIRONMENT_VARIABLE, "")
+    roots = [Path(item).expanduser() for item in listed.split(os.pathsep) if item]
+    roots += [(home or Path.home()) / ".local" / "share" / "radeon-kernels" / "packs",
+              (prefix or Path(sys.prefix)) / "share" / "radeon-kernels" / "packs"]
     if include_in_tree:
-        candidates.append(IN_TREE_PACK_ROOT)
-    roots: list[Path] = []
-    for candidate in candidates:
-        absolute = candidate.absolute()
-        if absolute not in roots:
-            roots.append(absolute)
-    return tuple(roots)
+        roots.append(IN_TREE_PACK_ROOT)
+    return tuple(dict.fromkeys(root.absolute() for root in roots))  # first occurrence wins
 
 
 def pack_directories(roots: Iterable[Path]) -> tuple[Path, ...]:
-    found: list[Path] = []
-    for root in roots:
-        root = Path(root).expanduser()
+    """Every pack directory under ``roots``, resolved, in root order and without repeats."""
+
+    def packs_in(root: Path) -> list[Path]:
         if (root / "manifest.json").is_file():
-            children: Sequence[Path] = (root,)
-        elif root.is_dir():
-            children = [child for child in sorted(root.iterdir()) if (child / "manifest.json").is_file()]
-        else:
-            children = ()
-        for child in children:
-            resolved = child.resolve()
-            if resolved not in found:
-                found.append(resolved)
-    return tuple(found)
+            return [root]
+        if root.is_dir():
+            return [child for child in sorted(root.iterdir()) if (child / "manifest.json").is_file()]
+        return []
+
+    found = (child.resolve() for root in roots for child in packs_in(Path(root).expanduser()))
+    return tuple(dict.fromkeys(found))
 
 
 class KernelPackRegistry:
     def __init__(self, packs: Sequence[KernelPack] = (), *, rejected: Sequence[str] = ()) -> None:
         self._packs = tuple(packs)
         self._rejected = tuple(rejected)
+        self._index: dict[tuple[EnvironmentKey, str, str], list[tuple[KernelPack, KernelPackArtifact]]] = {}
+        for pack in self._packs:
+            for item in pack.artifacts:
+                slot = (pack.environment.key, item.operator, item.semantic_version)
+                self._index.setdefault(slot, []).append((pack, item))
 
     @classmethod
     def discover(
@@ -101,18 +99,17 @@ class KernelPackRegistry:
         require_signatures: bool = True,
         trusted_keys: TrustedKeyring | None = None,
     ) -> KernelPackRegistry:
-        packs: list[KernelPack] = []
-        rejected: list[str] = []
         keyring = trusted_keys
         if require_signatures and keyring is None:
             keyring = default_trusted_keyring()
+        packs, rejected = [], []
         for directory in pack_directories(roots):
             try:
                 if require_signatures:
                     verify_detached_file(directory / "manifest.json", directory / "manifest.sig.json", keyring,
                                          signed_file="manifest.json")
                 packs.append(KernelPack.from_directory(directory, verify_artifacts=False))
-            except (ConfigError, SignatureVerificationError, RadeonKernelsError) as error:
+            except RadeonKernelsError as error:  # a malformed manifest or a failed signature
                 rejected.append(f"{directory}: {error}")
         return cls(packs, rejected=rejected)
 
@@ -133,17 +130,9 @@ class KernelPackRegistry:
         artifact: ArtifactSpec,
         evidence_id: str,
     ) -> ResolvedKernelPack:
-        for pack in self._packs:
-            if not pack.matches(fingerprint):
-                continue
-            try:
-                item = pack.get(operator, semantic_version)
-            except ConfigError:
-                continue
-            if item.artifact == artifact and item.evidence_id == evidence_id:
+        for pack, item in self._index.get((fingerprint.key, operator, semantic_version), ()):
+            if pack.matches(fingerprint) and item.artifact == artifact and item.evidence_id == evidence_id:
                 return ResolvedKernelPack(pack=pack, artifact=item)
-        suffix = f"; {len(self._rejected)} invalid pack(s) were ignored" if self._rejected else ""
-        raise PackResolutionError(
-            f"no installed kernel pack matches {operator} {semantic_version}, "
-            f"{fingerprint.architecture}, ROCm {fingerprint.rocm_abi}{suffix}"
-        )
+        ignored = f"; {len(self._rejected)} invalid pack(s) were ignored" if self._rejected else ""
+        raise PackResolutionError(f"no installed kernel pack matches {operator} {semantic_version}, "
+                                  f"{fingerprint.architecture}, ROCm {fingerprint.rocm_abi}{ignored}")

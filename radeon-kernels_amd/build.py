@@ -268,8 +268,23 @@ def compile_launch_loops(verbose: bool = False) -> Path:
     return target
 
 
+def compile_read_probe(verbose: bool = False) -> Path:
+    """The read-only HBM probe program (benchmarks/read_probe.hip): no library, no torch."""
+
+    source = PACKAGE_ROOT / "benchmarks" / "read_probe.hip"
+    target = PACKAGE_ROOT / "benchmarks" / "read_probe"
+    temporary = PACKAGE_ROOT / "_build" / "read_probe"
+    temporary.parent.mkdir(exist_ok=True)
+    flags = [flag for flag in HIPCC_FLAGS if flag != "-fPIC"]
+    _finish(_run([_hipcc(), *flags, str(source), "-Wl,--build-id=none", "-o", str(temporary)], verbose),
+            "hipcc (read_probe.hip)")
+    os.replace(temporary, target)
+    return target
+
+
 def build(verbose: bool = False) -> dict:
     compile_launch_loops(verbose)
+    compile_read_probe(verbose)
     summary = write_pack_and_dispatch(compile_libraries(verbose=verbose))
     # Sign the pack manifest (the runtime loads only signed packs) and rewrite the promotion records
     # from the committed GPU evaluations (promotion/publish.py).

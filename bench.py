@@ -688,9 +688,10 @@ def main(argv=None) -> int:
         gen = torch.Generator(device=device).manual_seed(data["seed"] + 1)
         new_k = torch.randn((batch, hkv, d), generator=gen, device=device).to(q.dtype)
         new_v = torch.randn((batch, hkv, d), generator=gen, device=device).to(q.dtype)
-        pos = cl.long().clamp(max=mb * bs) - 1
-        safe = pos.clamp(min=0)
-        slots = torch.where(pos >= 0, bt.long().gather(1, (safe // bs).unsqueeze(1)).squeeze(1) * bs + safe % bs,
+        pos = cl.long() - 1  # no slot (-1) for an empty context or one past the table, as the decode treats them
+        safe = pos.clamp(min=0, max=mb * bs - 1)
+        slots = torch.where((pos >= 0) & (pos < mb * bs),
+                            bt.long().gather(1, (safe // bs).unsqueeze(1)).squeeze(1) * bs + safe % bs,
                             torch.full_like(pos, -1))
         appends = [kvlib.prepare_append(new_k, new_v, kc, vc, slots, stream=stream) for kc, vc in caches]
         fused_steps = [lib.prepare(q, kc, vc, bt, cl, partition_tokens=partition, variant=variant, out=out,

@@ -158,10 +158,11 @@ int rk_pa_decode_fused(const void* query, const void* key_cache, const void* val
  *
  * Preconditions beyond rk_pa_decode's: no other sequence of the call attends to a new token's slot
  * (each new token lies in its own sequence's tail block, as paged serving allocates them).  A
- * context length <= 0 appends nothing; one above max_blocks_per_sequence * block_size is clamped
- * to it first, as the decode clamps it, so the new token takes the table's last position; a new
- * token whose block id is outside [0, num_blocks) is not stored and is masked, as the append and
- * the decode each treat it.
+ * context length <= 0 appends nothing.  One above max_blocks_per_sequence * block_size puts the new
+ * token outside the table: it is neither stored nor attended, and the call attends over the
+ * table's max_blocks_per_sequence * block_size tokens exactly as rk_pa_decode does (the decode
+ * clamps the context length there).  A new token whose block id is outside [0, num_blocks) is not
+ * stored and is masked, as the append and the decode each treat it.
  *
  * counters/counter_words: NULL for the two-launch form (partition kernel, then the reduce kernel
  * when a sequence can span several partitions), or the counters of rk_pa_decode_fused for the

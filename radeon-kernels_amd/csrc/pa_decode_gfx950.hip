@@ -38,6 +38,7 @@
 
 #include <mutex>
 #include <string>
+#include <utility>
 
 #include "rk_paged_attention.h"
 
@@ -215,6 +216,17 @@ template <int N>
 struct Int {
   static constexpr int value = N;
 };
+
+// f(Int<0>{}), ..., f(Int<N - 1>{}) in order: a loop whose index is a compile-time constant in the
+// body, so that register arrays indexed by it stay in registers.
+template <class F, int... K>
+__device__ __forceinline__ void unroll_each(F&& f, std::integer_sequence<int, K...>) {
+  (f(Int<K>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void unroll(F&& f) {
+  unroll_each(f, std::make_integer_sequence<int, N>{});
+}
 
 __device__ __forceinline__ int64_t load_index(const void* base, int64_t i, bool is64) {
   return is64 ? static_cast<const int64_t*>(base)[i]
@@ -443,6 +455,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   // per SIMD) and for blocks smaller than a tile (per-lane block-table reads in LDS).
   constexpr int DEPTH = (QK_MFMA && UB && D != 256) ? 2 : 1;
   constexpr int SLOTS = DEPTH + 1;
+  static_assert(UB || DEPTH == 1, "tiles past the first need their block ids before the table is staged");
   // Vector memory instructions one tile issues (K DMA or K rows, then V rows): the unit of the
   // explicit memory-counter waits.
   constexpr int ROW_LOADS = 4 * (VW >= 4 ? VW / 4 : 1);
@@ -560,13 +573,12 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 
   // Block ids of this wave's first DEPTH tiles (tokens p0 + 16 * wave + 64 * n), read straight from
   // the table so they can be issued before the staged slice is visible to the wave.
-  RawIndex first_raw[2] = {{~0u, ~0u}, {~0u, ~0u}};
-  if constexpr (UB) {
+  RawIndex first_raw[DEPTH];
 #pragma unroll
-    for (int n = 0; n < DEPTH; ++n) {
-      const int idx = ((p0 + wave * kTile + n * kWaves * kTile) >> lb) - blk0;
-      if (idx < slice) first_raw[n] = load_raw_index(p.block_tables, table_row + idx, is64);
-    }
+  for (int n = 0; n < DEPTH; ++n) {
+    first_raw[n] = RawIndex{~0u, ~0u};
+    const int idx = ((p0 + wave * kTile + n * kWaves * kTile) >> lb) - blk0;
+    if (UB && idx < slice) first_raw[n] = load_raw_index(p.block_tables, table_row + idx, is64);
   }
   auto valid_block = [&](RawIndex r) -> int {
     const int64_t id = index_value(r, is64);
@@ -594,9 +606,11 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     return;
   }
   const int p_end = static_cast<int>(min(static_cast<int64_t>(p0 + P), ctx));
-  // Append: the new token's position, and whether this partition holds it (the last one does).
+  // Append: the new token's position, and whether this partition holds it (the last one does).  A
+  // context length past the table puts the new token outside it: it is neither stored nor read, and
+  // the partitions cover the table's tokens as they do without an append.
   const int ap_pos = static_cast<int>(ctx - 1);
-  const bool ap_here = AP && ap_pos >= p0 && ap_pos < p_end;
+  const bool ap_here = AP && ctx_len <= max_ctx && ap_pos >= p0 && ap_pos < p_end;
 
   // Stage this partition's block-table slice in LDS (-1 marks ids outside [0, num_blocks)).  It is
   // made visible by the barrier in front of the main loop.
@@ -650,7 +664,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   }
   const uint32_t table_lds = lds_address(s_table);
 
-  auto load_v_rows = [&](uint32_t (&dst)[4][VW], const uint16_t* const src[4]) {
+  auto load_v_rows = [&](uint32_t (&dst)[4][VW], const uint16_t* const src[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       if constexpr (VW == 2) {
@@ -671,7 +685,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   // Issue every load of the tile starting at token t0: K into LDS slot `slot` (MFMA variant) or
   // registers (VALU variant), V into registers.
   // Uniform-block form: `pb` is the tile's block id (-1 when invalid).
-  auto issue_tile_block = [&](Tile& tile, int slot, int t0, int pb) {
+  auto issue_tile_block = [&](Tile& tile, int slot, int t0, int pb) __attribute__((always_inline)) {
     const uint16_t* vrow[4];
     const uint16_t* krow[4];
     if constexpr (UB) {
@@ -745,7 +759,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     if constexpr (!QK_MFMA) load_v_rows(tile.kr, krow);  // K rows of masked tokens need no zeroing
     load_v_rows(tile.v, vrow);
   };
-  auto issue_tile = [&](Tile& tile, int slot, int t0) {
+  auto issue_tile = [&](Tile& tile, int slot, int t0) __attribute__((always_inline)) {
     int pb = -1;
     if constexpr (UB) {
       const int t_tab = min(t0, last);  // a tile past the partition end reads a valid table entry
@@ -767,7 +781,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 
   // Scores of tokens 4g..4g+3 for head my_head, base-2 scaled, -inf where masked.  Branch-free
   // (the full-tile shortcut is a select) so no control flow sits between the tile's wait and its use.
-  auto qk_phase = [&](const Tile& tile, auto slot_tag, float (&x)[4]) {
+  auto qk_phase = [&](const Tile& tile, auto slot_tag, float (&x)[4]) __attribute__((always_inline)) {
     const bool FULL = tile.full;
     if constexpr (QK_MFMA) {
       constexpr int OFFSET = decltype(slot_tag)::value * SLOT_BYTES;
@@ -808,7 +822,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     }
   };
 
-  auto pv_phase = [&](const Tile& tile, const float (&x)[4], auto full_tag) {
+  auto pv_phase = [&](const Tile& tile, const float (&x)[4], auto full_tag) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full_tag)::value;
     // Tile maximum for my_head over the 16 tokens (4 registers x 4 lane groups).
     float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
@@ -883,7 +897,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   // precisely; with this wait ahead of every use it never has to.  The slot and register tile that
   // the new loads overwrite belong to the tile computed in the previous step, which is finished.
   auto step = [&](const Tile& cur, auto cur_slot, Tile& next, auto next_slot, int next_t0, auto has_next,
-                  auto pending) {
+                  auto pending) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(wait_vmcnt(decltype(pending)::value * TILE_OPS));
     __asm__ __volatile__("" ::: "memory");
     if constexpr (decltype(has_next)::value) issue_tile(next, decltype(next_slot)::value, next_t0);
@@ -902,18 +916,20 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   const int n_tiles = first < p_end ? (p_end - first + step_tokens - 1) / step_tokens : 0;
   auto t0_of = [&](int n) { return first + n * step_tokens; };
   constexpr Flag<true> kIssue{};
-  constexpr Flag<false> kNoIssue{};
-  Tile ta, tb, tc;
+  Tile tiles[SLOTS];  // tile n lives in tiles[n % SLOTS] and K slot n % SLOTS
   // The first DEPTH tiles go out before the barrier that publishes the staged table (uniform-block
-  // path: their block ids were read directly).  With DEPTH 2 the second tile is issued even when it
-  // does not exist (its tokens then read as masked stand-ins of the first tile's block and it is
-  // never computed): an unconditional issue keeps the compiler's view of the memory counter
-  // identical on every path into the loop, so it adds no waits of its own.
+  // path: their block ids were read directly).  All DEPTH are issued even when fewer tiles exist (a
+  // missing tile reads masked stand-in rows of the first tile's block and is never computed): an
+  // unconditional issue keeps the compiler's view of the memory counter identical on every path
+  // into the loop, so it adds no waits of its own, and the explicit waits below only wait longer.
   if constexpr (UB) {
     if (n_tiles > 0) {
       const int pb0 = valid_block(first_raw[0]);
-      issue_tile_block(ta, 0, t0_of(0), pb0);
-      if constexpr (DEPTH == 2) issue_tile_block(tb, 1, t0_of(1), t0_of(1) <= last ? valid_block(first_raw[1]) : pb0);
+      unroll<DEPTH>([&](auto n) __attribute__((always_inline)) {
+        constexpr int N = decltype(n)::value;
+        const int t0 = t0_of(N);
+        issue_tile_block(tiles[N], N, t0, (N == 0 || t0 <= last) ? valid_block(first_raw[N]) : pb0);
+      });
     }
   }
   lds_barrier();
@@ -932,48 +948,37 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     }
   }
   if constexpr (!UB) {
-    if (n_tiles > 0) issue_tile(ta, 0, t0_of(0));
+    if (n_tiles > 0) issue_tile(tiles[0], 0, t0_of(0));
   }
-  if constexpr (DEPTH == 2) {
-    if (n_tiles > 0) {
-      int n = 0;
-      for (; n + 5 <= n_tiles; n += 3) {
-        step(ta, Int<0>{}, tc, Int<2>{}, t0_of(n + 2), kIssue, Int<1>{});
-        step(tb, Int<1>{}, ta, Int<0>{}, t0_of(n + 3), kIssue, Int<1>{});
-        step(tc, Int<2>{}, tb, Int<1>{}, t0_of(n + 4), kIssue, Int<1>{});
+
+  // Step K of a run of steps that starts at tile n (a multiple of SLOTS): computes tile n + K from
+  // slot K % SLOTS and, when ISSUE, first sends out tile n + K + DEPTH into the slot of tile
+  // n + K - 1, computed in the step before.  PENDING tiles issued after n + K are still allowed in
+  // flight at its wait.
+  auto run_step = [&](auto k, int n, auto issue, auto pending) __attribute__((always_inline)) {
+    constexpr int K = decltype(k)::value;
+    constexpr int CUR = K % SLOTS;
+    constexpr int NEXT = (K + DEPTH) % SLOTS;
+    step(tiles[CUR], Int<CUR>{}, tiles[NEXT], Int<NEXT>{}, t0_of(n + K + DEPTH), issue, pending);
+  };
+  if (n_tiles > 0) {
+    int n = 0;
+    for (; n + SLOTS + DEPTH <= n_tiles; n += SLOTS)
+      unroll<SLOTS>([&](auto k) __attribute__((always_inline)) { run_step(k, n, kIssue, Int<DEPTH - 1>{}); });
+    // 1 to SLOTS + DEPTH - 1 tiles remain; min(left, DEPTH) of them are in flight.  Step K issues
+    // tile n + K + DEPTH if it exists; at its wait, min(DEPTH - 1, left - 1 - K) tiles after n + K
+    // have been issued.
+    const int left = n_tiles - n;
+    unroll<SLOTS + DEPTH - 1>([&](auto l) __attribute__((always_inline)) {
+      constexpr int L = decltype(l)::value + 1;
+      if (left == L) {
+        unroll<L>([&](auto k) __attribute__((always_inline)) {
+          constexpr int K = decltype(k)::value;
+          constexpr int AHEAD = L - 1 - K < DEPTH - 1 ? L - 1 - K : DEPTH - 1;
+          run_step(k, n, Flag<(K + DEPTH < L)>{}, Int<AHEAD>{});
+        });
       }
-      // 1 to 4 tiles remain; tiles n and n + 1 (if it exists) are already in flight.
-      const int left = n_tiles - n;
-      if (left == 1) {
-        step(ta, Int<0>{}, tc, Int<2>{}, 0, kNoIssue, Int<0>{});
-      } else if (left == 2) {
-        step(ta, Int<0>{}, tc, Int<2>{}, 0, kNoIssue, Int<1>{});
-        step(tb, Int<1>{}, ta, Int<0>{}, 0, kNoIssue, Int<0>{});
-      } else if (left == 3) {
-        step(ta, Int<0>{}, tc, Int<2>{}, t0_of(n + 2), kIssue, Int<1>{});
-        step(tb, Int<1>{}, ta, Int<0>{}, 0, kNoIssue, Int<1>{});
-        step(tc, Int<2>{}, tb, Int<1>{}, 0, kNoIssue, Int<0>{});
-      } else {
-        step(ta, Int<0>{}, tc, Int<2>{}, t0_of(n + 2), kIssue, Int<1>{});
-        step(tb, Int<1>{}, ta, Int<0>{}, t0_of(n + 3), kIssue, Int<1>{});
-        step(tc, Int<2>{}, tb, Int<1>{}, 0, kNoIssue, Int<1>{});
-        step(ta, Int<0>{}, tc, Int<2>{}, 0, kNoIssue, Int<0>{});
-      }
-    }
-  } else {
-    if (n_tiles > 0) {
-      int n = 0;
-      for (; n + 2 < n_tiles; n += 2) {
-        step(ta, Int<0>{}, tb, Int<1>{}, t0_of(n + 1), kIssue, Int<0>{});
-        step(tb, Int<1>{}, ta, Int<0>{}, t0_of(n + 2), kIssue, Int<0>{});
-      }
-      if (n + 1 < n_tiles) {
-        step(ta, Int<0>{}, tb, Int<1>{}, t0_of(n + 1), kIssue, Int<0>{});
-        step(tb, Int<1>{}, ta, Int<0>{}, 0, kNoIssue, Int<0>{});
-      } else {
-        step(ta, Int<0>{}, tb, Int<1>{}, 0, kNoIssue, Int<0>{});
-      }
-    }
+    });
   }
 
   // Wave totals: sum the four lane groups (they hold disjoint tokens, identical maxima).

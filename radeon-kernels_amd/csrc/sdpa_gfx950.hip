@@ -10,7 +10,7 @@
 //
 //   sdpa_fwd_kernel  one 256-thread workgroup per (sequence, query head, block of 128 queries);
 //                    each of its 4 waves owns 32 queries and walks the keys in blocks of BN (64, or
-//                    32 for head_dim 256 and for head_dim-128 grids of several rounds).  K and V
+//                    32 for head_dim 256).  K and V
 //                    tiles reach LDS by DMA (global_load_lds_dwordx4, no staging registers),
 //                    double-buffered: block n + 1 loads while block n is computed, with one
 //                    LDS-only barrier per block.  Rows are unpadded and XOR-swizzled in 16-byte
@@ -134,7 +134,7 @@ struct Tiling {
   static_assert(BN == 32 || BN == 64, "32 or 64 keys per block");
   static_assert(D != 256 || BN == 32, "head_dim 256 uses 32-key blocks");
   static constexpr int kBlockN = BN;
-  static constexpr int kOccupancy = D == 256 ? 1 : (D == 128 && BN == 32 ? 3 : 2);
+  static constexpr int kOccupancy = D == 256 ? 1 : 2;  // resident workgroups per CU
   static constexpr int kRowBytes = D * 2;
   static constexpr int kTileBytes = kBlockN * kRowBytes;  // one K or V tile
   static constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;  // 1 KB per DMA instruction
@@ -538,8 +538,16 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-// Grids above one round of three workgroups on each of the 256 CUs take the XCD-owned grid order.
-constexpr int64_t kWideGrid = 3 * 256;
+// Workgroups resident at once on the 256 CUs for the instantiation a head_dim launches: grids larger
+// than this run several rounds and take the XCD-owned grid order.
+constexpr int64_t kCus = 256;
+int64_t one_round(int64_t head_dim) {
+  switch (head_dim) {
+    case 64: return Tiling<64, 64>::kOccupancy * kCus;
+    case 128: return Tiling<128, 64>::kOccupancy * kCus;
+    default: return Tiling<256, 32>::kOccupancy * kCus;
+  }
+}
 
 template <class E, int D, int BN>
 void launch_d(const Params& prm, bool causal, dim3 grid, hipStream_t stream) {
@@ -583,8 +591,8 @@ extern "C" int rk_sdpa_forward(const void* query, const void* key, const void* v
   if (!aligned16(query) || !aligned16(key) || !aligned16(value) || !aligned16(output))
     return fail(RK_SDPA_ERR_UNSUPPORTED, "query, key, value and output must be 16-byte aligned");
   const int64_t q_blocks = (sequence + kBlockM - 1) / kBlockM;
-  if (batch * query_heads >= 65536 || q_blocks >= 65536 ||
-      batch * query_heads * sequence * head_dim >= (int64_t{1} << 62) || sequence >= (int64_t{1} << 30))
+  if (sequence >= (int64_t{1} << 30) || batch >= (int64_t{1} << 31) || query_heads >= (int64_t{1} << 31) ||
+      batch * query_heads > ((int64_t{1} << 62) - 1) / sequence / head_dim)
     return fail(RK_SDPA_ERR_UNSUPPORTED, "shape exceeds the launch limits of this kernel");
 
   Params prm{};
@@ -607,7 +615,10 @@ extern "C" int rk_sdpa_forward(const void* query, const void* key, const void* v
   const int64_t slices = 8 / std::gcd(groups, int64_t{8});
   const int64_t slice_items = (query_heads / kv_heads) * ((q_blocks + slices - 1) / slices);
   const int64_t grid_1d = groups * slices * slice_items;
-  const bool sliced = workgroups > kWideGrid && grid_1d < (int64_t{1} << 31);
+  const bool sliced = workgroups > one_round(head_dim) && grid_1d < (int64_t{1} << 31);
+  // The two-dimensional grid holds (sequence x head, query block) in its y and x extents.
+  if (!sliced && (batch * query_heads >= 65536 || q_blocks >= 65536))
+    return fail(RK_SDPA_ERR_UNSUPPORTED, "shape exceeds the launch limits of this kernel");
   prm.xcd_slices = sliced ? static_cast<int32_t>(slices) : 0;
   prm.slice_items = static_cast<int32_t>(slice_items);
   const dim3 grid = sliced ? dim3(static_cast<uint32_t>(grid_1d))

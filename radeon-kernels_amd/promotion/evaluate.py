@@ -21,7 +21,10 @@ which also evaluates every exact winner on its own workload:
   fallback function on the same inputs; each sample is the mean over a batch of back-to-back calls
   bracketed by HIP events, the batch size calibrated to about 10 ms (at most 1000 calls) on the
   faster side and shared by both, and the order of the pair alternates from sample to sample; a
-  second of untimed alternating batches precedes the samples, and a set of samples in which either
+  second of untimed alternating batches precedes the samples, every timed batch follows about 20 ms
+  of untimed calls of the same side (so it measures that side's steady state whichever side ran
+  before it -- a departure from the reference's loop, whose samples carry that order effect), and a
+  set of samples in which either
   side exceeds the 3% CV gate is taken again (at most three sets; the count is recorded).  The
   candidate is the entry's kernel launch through its C-ABI entry point, issued from a C loop
   (promotion/launch_loop.c: the launch the pack binding makes, without one Python call per launch);
@@ -59,6 +62,7 @@ ROTATION_BYTES = 768e6  # > 3x the 256 MB last-level cache
 SETTLE_SECONDS = 1.0
 MAXIMUM_CV = 0.03  # the promotion gate (benchmarks/workloads/*-1.0.yaml: maximum_cv)
 MAX_ATTEMPTS = 3
+LEAD_MS = 20.0  # untimed calls of a side before each of its timed batches
 # Oracle and baseline names of benchmarks/workloads/<operator>-1.0.yaml:4-5.
 METHODS = {"paged_attention_decode": "torch_fp32_paged_reference", "kv_cache_append": "torch_index_copy",
            "kv_cache_copy": "torch_snapshot_index_copy", "sdpa": "torch_fp32_explicit_attention"}
@@ -144,9 +148,14 @@ def time_pair(torch, candidate, baseline, *, samples: int, copies: int = 1) -> d
     def whole(n: int) -> int:
         return unit * math.ceil(n / unit)
 
-    def one(side, n):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    def one(side, n, lead=0):
+        """ms per call of n timed calls, after `lead` untimed calls of the same side."""
+
         first = cursor.get(id(side), 0)
+        if lead:
+            side.batch(first, lead)
+            first = (first + lead) % copies
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         side.batch(first, n)
         end.record()
@@ -163,8 +172,14 @@ def time_pair(torch, candidate, baseline, *, samples: int, copies: int = 1) -> d
     while time.perf_counter() - settle_start < SETTLE_SECONDS:
         one(candidate, whole(200))
         one(baseline, whole(5))
-    fastest = min(one(candidate, whole(3)), one(baseline, whole(3)))
-    calls = whole(max(1, min(1000, math.ceil(10.0 / max(fastest, 1e-6)))))
+    per_call = {id(side): one(side, whole(3)) for side in (candidate, baseline)}
+    calls = whole(max(1, min(1000, math.ceil(10.0 / max(min(per_call.values()), 1e-6)))))
+    # Every timed batch starts after about LEAD_MS of untimed calls of the same side, so that it
+    # measures that side's steady state whichever side ran before it: a microsecond-scale kernel
+    # that followed the host-bound fallback (the GPU idle meanwhile) measured 6% slower than one that
+    # followed itself, which alone put its samples near the CV gate; 1 ms of lead-in did not remove
+    # the difference.
+    lead = {key: whole(max(1, math.ceil(LEAD_MS / max(ms, 1e-6)))) for key, ms in per_call.items()}
 
     def stats(values):
         mean = statistics.fmean(values)
@@ -178,12 +193,13 @@ def time_pair(torch, candidate, baseline, *, samples: int, copies: int = 1) -> d
         for index in range(samples):
             pairs = ((candidate, c), (baseline, b)) if index % 2 == 0 else ((baseline, b), (candidate, c))
             for side, out in pairs:
-                out.append(one(side, calls))
+                out.append(one(side, calls, lead[id(side)]))
         result = {"candidate": stats(c), "baseline": stats(b)}
         if max(result["candidate"]["coefficient_of_variation"],
                result["baseline"]["coefficient_of_variation"]) <= MAXIMUM_CV:
             break
     return {**result, "calls_per_sample": calls, "copies": copies, "attempts": attempt,
+            "lead_calls": {"candidate": lead[id(candidate)], "baseline": lead[id(baseline)]},
             "candidate_method": CANDIDATE_METHOD + candidate.note, "baseline_replay": baseline.note.strip(", ")}
 
 

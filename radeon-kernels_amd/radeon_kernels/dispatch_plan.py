@@ -188,11 +188,14 @@ SDPA_EXACT_REGIONS: list[tuple[str, dict[str, Any]]] = [
         ("b2-gqa16x4-s256-d256-causal", 2, 16, 4, 256, 256, True),
     )
 ]
+# Every shape of the box launches natively: grids of one round (<= 512 workgroups) take the 2-D order,
+# larger ones the 1-D XCD-owned order, whose grid of at most batch * query_heads * (ceil(sequence / 128)
+# + 7) workgroups stays below 2^31 here (1024 * 256 * 4103); the element count stays below 2^62.
 SDPA_BROAD_REGION: dict[str, Any] = {
-    "batch": [1, 65535],
-    "query_heads": [1, 65535],
-    "kv_heads": [1, 65535],
-    "sequence": [1, (1 << 30) - 1],
+    "batch": [1, 1024],
+    "query_heads": [1, 256],
+    "kv_heads": [1, 256],
+    "sequence": [1, 1 << 19],
     "head_dim": {"one_of": [64, 128, 256]},
     "attention_mode": {"one_of": ["causal", "noncausal"]},
 }

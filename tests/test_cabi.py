@@ -382,7 +382,10 @@ def test_sdpa_header_and_library_agree(sdpalib):
     (dict(is_causal=2), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "is_causal"),
     (dict(scale=float("nan")), cabi.RK_SDPA_ERR_INVALID_ARGUMENT, "positive and finite"),
     (dict(output=104), cabi.RK_SDPA_ERR_UNSUPPORTED, "16-byte aligned"),
-    (dict(batch=1024, query_heads=64, kv_heads=8), cabi.RK_SDPA_ERR_UNSUPPORTED, "launch limits"),
+    (dict(sequence=1 << 30), cabi.RK_SDPA_ERR_UNSUPPORTED, "launch limits"),
+    # 2^24 (sequence, head) rows of 128 query blocks: 2^31 workgroups, too many for either grid order.
+    (dict(batch=4096, query_heads=4096, kv_heads=4096, sequence=16384), cabi.RK_SDPA_ERR_UNSUPPORTED,
+     "launch limits"),
 ])
 def test_sdpa_invalid_arguments_are_rejected_before_launch(sdpalib, overrides, status, message):
     args = dict(query=16, key=32, value=48, output=96, batch=1, query_heads=8, kv_heads=2, sequence=64,
@@ -390,3 +393,22 @@ def test_sdpa_invalid_arguments_are_rejected_before_launch(sdpalib, overrides, s
     args.update(overrides)
     assert sdpalib.forward_raw(**args) == status
     assert message in sdpalib.last_error()
+
+
+@cpu_only
+@pytest.mark.parametrize("batch, query_heads, kv_heads, sequence, head_dim", [
+    (1024, 64, 8, 64, 128),      # 65536 (sequence, head) rows: past the 2-D grid, fine for the 1-D one
+    (1, 65536, 65536, 128, 64),
+    (1024, 256, 256, 1 << 19, 256),  # the corner of the broad dispatch region
+])
+def test_sdpa_grids_past_the_two_dimensional_limits_are_launched(sdpalib, batch, query_heads, kv_heads, sequence,
+                                                                 head_dim):
+    """Grids of several rounds take the one-dimensional XCD-owned order, which has no 65536 limit on
+    (sequence x head) rows or query blocks: validation accepts them, and without a GPU the launch
+    itself is what fails."""
+
+    got = sdpalib.forward_raw(query=16, key=32, value=48, output=96, batch=batch, query_heads=query_heads,
+                              kv_heads=kv_heads, sequence=sequence, head_dim=head_dim, is_causal=1, scale=0.125,
+                              dtype=cabi.RK_DTYPE_BF16, stream=0)
+    assert got == cabi.RK_SDPA_ERR_LAUNCH, sdpalib.last_error()
+    assert "sdpa launch failed" in sdpalib.last_error()

@@ -21,13 +21,15 @@ WORKLOAD_PARTITIONS = {"c1": 128, "c2": 256, "c3": 512, "c4": 128, "c5": 2048}
 
 
 def new_token_slots(torch, block_tables, context_lengths, block_size):
-    """Slot of position context_length - 1 (clamped to the table), or -1 for an empty context."""
+    """Slot of position context_length - 1, or -1 (nothing appended) for an empty context and for a
+    context past the table's max_blocks * block_size tokens."""
 
     limit = block_tables.shape[1] * block_size
-    pos = context_lengths.long().clamp(max=limit) - 1
-    safe = pos.clamp(min=0)
+    pos = context_lengths.long() - 1
+    inside = (pos >= 0) & (pos < limit)
+    safe = pos.clamp(min=0, max=limit - 1)
     block = block_tables.long().gather(1, (safe // block_size).unsqueeze(1)).squeeze(1)
-    return torch.where(pos >= 0, block * block_size + safe % block_size, torch.full_like(pos, -1))
+    return torch.where(inside, block * block_size + safe % block_size, torch.full_like(pos, -1))
 
 
 def new_rows(torch, query, kv_heads, seed):
@@ -131,9 +133,10 @@ def test_invalid_new_token_block_is_skipped_and_masked(gpu, palib, kvlib, index_
 
 
 @pytest.mark.parametrize("phase", ["all", "fused"])
-def test_context_past_the_table_appends_at_its_last_position(gpu, palib, kvlib, phase):
-    """A context length above max_blocks * block_size is clamped first, as the decode clamps it: the
-    new token takes the table's last position."""
+def test_context_past_the_table_appends_nothing(gpu, palib, kvlib, phase):
+    """A context length above max_blocks * block_size puts the new token outside the table: the call
+    stores nothing for that sequence (its table's tokens, the last one included, stay as they were)
+    and attends over the table's tokens, as the decode alone does."""
 
     import torch
 

@@ -101,11 +101,16 @@ def test_shapes_and_tails(gpu, sdpalib, shape, dtype):
     check(out.cpu(), q, k, v, causal, dtype, what=f"{shape}/{dtype}")
 
 
-# Grids of more than 768 workgroups (three rounds' worth on 256 CUs) take the XCD-owned grid order;
-# the shapes above all launch fewer.  B, Hq, Hkv, S, D, causal; workgroups = B * Hq * ceil(S / 128).
-# They take the XCD-owned grid order: each KV group cut into 8 / gcd(groups, 8) slices of query blocks
-# (with padding workgroups when the slices are uneven).
+# Grids of more than one round -- 512 workgroups for head_dim 64 and 128 (two per CU), 256 for
+# head_dim 256 (one per CU) -- take the XCD-owned grid order; the shapes above all launch one round or
+# less.  B, Hq, Hkv, S, D, causal; workgroups = B * Hq * ceil(S / 128).  Each KV group is cut into
+# 8 / gcd(groups, 8) slices of query blocks (with padding workgroups when the slices are uneven).
+ONE_ROUND = {64: 512, 128: 512, 256: 256}
 WIDE = [
+    (3, 32, 8, 700, 128, False),   # 576: two rounds, the smallest multi-round range, 24 KV groups
+    (5, 24, 6, 600, 64, True),     # 600, 30 KV groups (4 slices, padding)
+    (2, 32, 8, 600, 256, True),    # 320, head_dim 256: past its one round of 256, 16 KV groups
+    (3, 16, 4, 700, 256, False),   # 288, head_dim 256, 12 KV groups (2 slices)
     (4, 32, 8, 1024, 128, True),   # 1024 workgroups, 32 KV groups (1 slice each)
     (5, 64, 8, 300, 128, False),   # 960, ragged tail block, 40 KV groups
     (3, 96, 12, 333, 128, True),   # 864, ragged, group of 8, 36 KV groups (2 slices, padding)
@@ -127,7 +132,7 @@ def test_wide_grids(gpu, sdpalib, shape, dtype):
     import torch
 
     b, hq, hkv, s, d, causal = shape
-    assert b * hq * -(-s // 128) > 768
+    assert b * hq * -(-s // 128) > ONE_ROUND[d]
     q, k, v = make(torch, b, hq, hkv, s, d, dtype, seed=b * 7 + hq + s)
     announce(f"sdpa wide grid {shape} {dtype}")
     out = sdpalib.forward(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal).cpu()

@@ -85,13 +85,18 @@ def parse_args(argv=None):
     return parser.parse_args(argv)
 
 
+PUBLIC_CALLS_MIN = 200
+
+
 def public_call_us(torch, call, steps: int, batches: int = 5) -> float:
     """Host wall time per call of the public operator: the median of ``batches`` batches of ``steps``
-    back-to-back calls, each batch closed by a synchronisation (single batches were seen to catch
-    one-off host stalls of the box)."""
+    (at least PUBLIC_CALLS_MIN) back-to-back calls, each batch closed by a synchronisation (single
+    batches were seen to catch one-off host stalls of the box; batches of 10 calls added the two
+    synchronisations, 2-3 us, to every microsecond-scale call)."""
 
     import statistics
 
+    steps = max(steps, PUBLIC_CALLS_MIN)
     times = []
     for _ in range(batches):
         torch.cuda.synchronize()

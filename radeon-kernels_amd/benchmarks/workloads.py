@@ -6,7 +6,7 @@ context lengths are drawn.  Inputs are drawn on the CPU, so a seed names one inp
 machine, in a fixed order: context lengths, block permutation, query, keys, values.
 
 * ``draw="serial"``: every tensor from one ``torch.Generator`` seeded with the workload seed.
-* ``draw="chunked"`` (the 4.8 GB ragged workload): context lengths, permutation and query as above;
+* ``draw="chunked"`` (the 4.24 GB ragged workload): context lengths, permutation and query as above;
   each cache is drawn in fixed chunks of ``CHUNK_ELEMENTS`` values, chunk ``i`` of cache ``c``
   (0 = keys, 1 = values) from its own generator seeded ``chunk_seed(seed, c, i)``.  The chunks are
   independent, so they are drawn on a thread pool; the result does not depend on the number of

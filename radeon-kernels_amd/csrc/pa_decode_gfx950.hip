@@ -48,8 +48,6 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kTile = 16;             // tokens per wave step = MFMA M
-constexpr int kXcds = 8;              // accelerator complex dies; workgroup h runs on XCD h % 8
-constexpr int64_t kXcdGroupedItems = 4096;
 constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, plus one straddle
 constexpr float kLog2e = 1.4426950408889634f;
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory operations are
@@ -281,7 +279,6 @@ struct Params {
   int32_t bs_log2;
   int32_t partition_tokens;
   int32_t num_partitions;  // ceil(max_blocks * BS / partition_tokens)
-  int32_t xcd_grouped;     // 1: head slots of a work item share an XCD (grid padded to whole rounds)
   int32_t index_is64;
   float scale_log2e;
 };
@@ -481,26 +478,15 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   u32x4* const s_k = reinterpret_cast<u32x4*>(s_raw) + wave * SLOTS * KTILE16;
   float(*const s_acc)[GC][D] = reinterpret_cast<float(*)[GC][D]>(s_raw);
 
-  // Workgroup -> (partition, sequence, KV head, head chunk).  Work items are ordered head slot
-  // (KV head, head chunk) fastest, then sequence, then partition, and the hardware id is mapped so
-  // that all head slots of one (sequence, partition) run on the same XCD while successive
-  // (sequence, partition) items go round-robin over the 8 XCDs (the dispatcher places hardware
-  // workgroup h on XCD h % 8).  The cache rows of a token are adjacent in memory across KV heads,
-  // so one XCD then requests each token's rows together (measured +2% over spreading the head slots
-  // over XCDs, +13% for partition-slowest over partition-fastest on the 128-sequence ragged
-  // workload); partition-major order lets the early-exiting workgroups of short sequences cluster
-  // at the end of the grid.  The host pads the grid to a multiple of 8 * head slots; padding
-  // workgroups (item index past the end) exit at once.  Grids of fewer than kXcdGroupedItems items
-  // (one or two rounds of workgroups, latency-bound) keep the identity mapping, which measured
-  // about 0.5 us faster there.
-  const int64_t heads_per_seq64 = static_cast<int64_t>(p.kv_heads) * p.head_chunks;
-  const int64_t hw = blockIdx.x;
-  int64_t wg = hw;
-  if (p.xcd_grouped) {
-    const int64_t hw_row = hw / kXcds;
-    wg = ((hw_row / heads_per_seq64) * kXcds + hw % kXcds) * heads_per_seq64 + hw_row % heads_per_seq64;
-    if (wg >= heads_per_seq64 * p.batch * p.num_partitions) return;
-  }
+  // Workgroup -> (partition, sequence, KV head, head chunk): head slot (KV head, head chunk)
+  // fastest, then sequence, then partition.  Partition-slowest order measured 13% faster than
+  // partition-fastest on the 128-sequence ragged workload, and it lets the early-exiting workgroups
+  // of short sequences cluster at the end of the grid.  The dispatcher places hardware workgroup h
+  // on XCD h % 8, so neighbouring head slots land on different XCDs.  Keeping all head slots of a
+  // (sequence, partition) on one XCD (their rows of a token are adjacent in memory) measured 1%
+  // slower than this identity order on that workload with non-temporal loads, as a read-only probe
+  // of the access pattern predicted; it had been 2% faster before them.
+  const int64_t wg = blockIdx.x;
   const int heads_per_seq = p.kv_heads * p.head_chunks;
   const int hslot = static_cast<int>(wg % heads_per_seq);
   const int64_t rest = wg / heads_per_seq;
@@ -1332,11 +1318,7 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   const int64_t group = query_heads / kv_heads;
   const int gc = head_chunk_for(group);
   const int64_t head_chunks = (group + gc - 1) / gc;
-  // Padded to whole rounds of (8 XCDs x head slots); the kernel maps hardware ids onto work items.
-  const int64_t xcd_round = kXcds * kv_heads * head_chunks;
-  const int64_t items = batch * kv_heads * head_chunks * s.num_partitions;
-  const bool xcd_grouped = items >= kXcdGroupedItems;
-  const int64_t grid = xcd_grouped ? (items + xcd_round - 1) / xcd_round * xcd_round : items;
+  const int64_t grid = batch * kv_heads * head_chunks * s.num_partitions;  // one workgroup per work item
   if (grid >= (int64_t{1} << 31))
     return fail(RK_ERR_UNSUPPORTED, "launch grid exceeds 2^31 workgroups");
 
@@ -1370,7 +1352,6 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.bs_log2 = log2_exact(block_size);
   prm.partition_tokens = static_cast<int32_t>(partition_tokens);
   prm.num_partitions = static_cast<int32_t>(s.num_partitions);
-  prm.xcd_grouped = xcd_grouped ? 1 : 0;
   prm.index_is64 = index_dtype == RK_INDEX_INT64 ? 1 : 0;
   prm.scale_log2e = scale * kLog2e;
 

@@ -72,9 +72,27 @@ extern "C" {
 #define RK_PA_VARIANT_VALU 1 /* fp32 FMAs + DPP row reductions */
 
 /*
- * Bytes of device workspace rk_pa_decode needs for this shape and partition size: split-K
- * partial (max, sum, accumulator) records, fp32.  Zero when one partition covers
- * max_blocks_per_sequence * block_size tokens (the single-pass launch needs none).
+ * Schedule of the partition kernel, OR-ed into the variant argument (no reference counterpart).
+ * Without either bit the library chooses: the work queue when the call is eligible for it and its
+ * work items (sequence x KV head x head chunk x partition) exceed the workgroups the device holds
+ * at once, else one workgroup per work item.  Both schedules compute every item the same way, so
+ * outputs are bit-identical.
+ *   RK_PA_SCHEDULE_GRID   one workgroup per work item, items past a sequence's context included
+ *                         (they exit at once).
+ *   RK_PA_SCHEDULE_QUEUE  as many workgroups as the device holds at once take the items that
+ *                         hold tokens from a ticket counter in the workspace header (a one-thread
+ *                         kernel zeroes it first).  Eligible: RK_PA_VARIANT_MFMA, a split-K shape
+ *                         (rk_pa_decode_workspace_bytes > 0) with at most 256 partitions per
+ *                         sequence and at most 1024 sequences; RK_ERR_UNSUPPORTED otherwise.
+ */
+#define RK_PA_SCHEDULE_GRID 0x100
+#define RK_PA_SCHEDULE_QUEUE 0x200
+
+/*
+ * Bytes of device workspace rk_pa_decode needs for this shape and partition size: a 256-byte
+ * header (the work-queue ticket counter) and the split-K partial (max, sum, accumulator) records,
+ * fp32.  Zero when one partition covers max_blocks_per_sequence * block_size tokens (the
+ * single-pass launch needs none).
  */
 int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t head_dim,
                                  int64_t block_size, int64_t max_blocks_per_sequence,
@@ -85,7 +103,7 @@ int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t hea
  *
  * partition_tokens: context tokens per workgroup (split-K partition); a multiple of 16 in
  *   [16, 8192] with partition_tokens / block_size <= 256.
- * variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_VALU.
+ * variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_VALU, optionally OR-ed with one RK_PA_SCHEDULE_* bit.
  * workspace/workspace_bytes: device buffer of at least rk_pa_decode_workspace_bytes(...) bytes
  *   (may be NULL/0 when that is zero).  Its contents need no initialisation.
  * stream: hipStream_t to launch on (NULL = the null stream).

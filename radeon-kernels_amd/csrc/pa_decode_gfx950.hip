@@ -36,6 +36,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -49,6 +50,10 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kTile = 16;             // tokens per wave step = MFMA M
 constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, plus one straddle
+// Work-queue schedule limits: sequences and partition levels whose item map fits in LDS.
+constexpr int kQueueMaxBatch = 1024;
+constexpr int kQueueMaxLevels = 256;
+constexpr size_t kQueueHeaderBytes = 256;  // workspace bytes in front of the split-K records
 constexpr float kLog2e = 1.4426950408889634f;
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory operations are
 // outstanding: vmcnt in bits [3:0] and [15:14], expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait on
@@ -260,6 +265,9 @@ struct Params {
   // Fused merge only (else null): [batch, kv_heads * head_chunks] arrival counters, zero on entry,
   // left zero on exit (the last arriver resets its counter).
   uint32_t* __restrict__ counters;
+  // Work-queue schedule only (else null): the ticket counter, zeroed by pa_queue_reset_kernel in
+  // front of every queue launch.
+  uint32_t* __restrict__ queue;
   // Append-and-decode only (else null): [batch, kv_heads, D] K and V rows of each sequence's new
   // token (position context_length - 1).  The kernel attends to them from these buffers and stores
   // them into that position's cache slot; k_store / v_store are the caches' base addresses.
@@ -433,8 +441,14 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
 //   Pipeline: DEPTH tiles are in flight ahead of the one being computed (DEPTH + 1 register tiles
 //   and LDS K slots rotate).  Step n: wait until tile n has landed -> issue tile n + DEPTH ->
 //   read K(n) from LDS -> MFMA -> softmax -> PV(n).
-template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP>
-__global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
+//
+// partition_item is one work item (sequence b, head slot = KV head * head_chunks + head chunk,
+// partition part) run by the whole workgroup (tid = threadIdx.x); the two kernels below differ only
+// in how they hand out work items.  at_loop_end() runs in every wave once the item's tiles are done,
+// before its epilogue.
+template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP, class LoopEnd>
+__device__ __attribute__((always_inline)) inline void partition_item(const Params& p, const int tid, int b, int hslot,
+                                                                     int part, LoopEnd&& at_loop_end) {
   static_assert(!AP || QK_MFMA, "append-and-decode is built for the MFMA variant");
   constexpr int KSTEPS = D / 32;       // MFMA k-steps; also DMA instructions per K tile
   constexpr int VEC = D / 16;          // elements of a token row per lane (row = 16 lanes)
@@ -470,7 +484,6 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   __shared__ float s_l[kWaves][GC];
   __shared__ int s_last;
 
-  const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4;   // lane group: owns tokens 4g..4g+3 of every tile (V / scores)
@@ -478,20 +491,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   u32x4* const s_k = reinterpret_cast<u32x4*>(s_raw) + wave * SLOTS * KTILE16;
   float(*const s_acc)[GC][D] = reinterpret_cast<float(*)[GC][D]>(s_raw);
 
-  // Workgroup -> (partition, sequence, KV head, head chunk): head slot (KV head, head chunk)
-  // fastest, then sequence, then partition.  Partition-slowest order measured 13% faster than
-  // partition-fastest on the 128-sequence ragged workload, and it lets the early-exiting workgroups
-  // of short sequences cluster at the end of the grid.  The dispatcher places hardware workgroup h
-  // on XCD h % 8, so neighbouring head slots land on different XCDs.  Keeping all head slots of a
-  // (sequence, partition) on one XCD (their rows of a token are adjacent in memory) measured 1%
-  // slower than this identity order on that workload with non-temporal loads, as a read-only probe
-  // of the access pattern predicted; it had been 2% faster before them.
-  const int64_t wg = blockIdx.x;
   const int heads_per_seq = p.kv_heads * p.head_chunks;
-  const int hslot = static_cast<int>(wg % heads_per_seq);
-  const int64_t rest = wg / heads_per_seq;
-  const int b = static_cast<int>(rest % p.batch);
-  const int part = static_cast<int>(rest / p.batch);
   const int kvh = hslot / p.head_chunks;
   const int chunk = hslot % p.head_chunks;
   const int head0 = kvh * p.group + chunk * GC;  // first query head of this chunk
@@ -967,6 +967,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
     });
   }
 
+  at_loop_end();
   // Wave totals: sum the four lane groups (they hold disjoint tokens, identical maxima).
   l_own = sum_xor16(l_own);
   l_own = sum_xor32(l_own);
@@ -1042,6 +1043,152 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   if (wave < heads_here) merge_partitions<E, D, true>(p, q_row0 + wave, np, lane);  // GC <= kWaves
 }
 
+// Grid schedule: one workgroup per work item, every item of the batch x head slots x partitions
+// space, the head slot fastest, then the sequence, then the partition.  Partition-slowest order
+// measured 13% faster than partition-fastest on the 128-sequence ragged workload, and it lets the
+// early-exiting workgroups of short sequences (partitions past their context) cluster at the end of
+// the grid.  The dispatcher places hardware workgroup h on XCD h % 8, so neighbouring head slots
+// land on different XCDs.  Keeping all head slots of a (sequence, partition) on one XCD (their rows
+// of a token are adjacent in memory) measured 1% slower than this identity order on that workload
+// with non-temporal loads, as a read-only probe of the access pattern predicted.
+template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP>
+__global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
+  const int64_t wg = blockIdx.x;
+  const int heads_per_seq = p.kv_heads * p.head_chunks;
+  const int hslot = static_cast<int>(wg % heads_per_seq);
+  const int64_t rest = wg / heads_per_seq;
+  const int b = static_cast<int>(rest % p.batch);
+  const int part = static_cast<int>(rest / p.batch);
+  partition_item<E, D, GC, QK_MFMA, UB, AP>(p, static_cast<int>(threadIdx.x), b, hslot, part, [] {});
+}
+
+// Work-queue schedule: as many workgroups as the device holds at once, each running work items
+// until none is left.  A grid of one workgroup per item pays a workgroup launch per item (the
+// per-workgroup timeline of the 128-sequence ragged workload showed 2-12 us between one
+// workgroup's end and the next one's start on the same CU) and a launch plus a context-length load
+// for every item past its sequence's context (3672 of its 8192 items, about 4 us each); here only
+// items with tokens are scheduled, and a workgroup's next item is claimed while its current one
+// finishes.
+//
+// Item map, built by every workgroup from the context lengths alone, so all agree on it: level k
+// holds partition k of every sequence with more than k partitions (a context <= 0 counts one
+// partition, whose item writes the NaN row), with the sequences ordered by partition count,
+// largest first (ties by index), and the head slot fastest.  Items are numbered level by level.
+// Level order keeps the grid schedule's partition-slowest walk; the count order inside a level puts
+// the sequences with the most work left first.
+//
+// Workgroup w runs item w first; every further item comes from the ticket counter
+// (gridDim.x + ticket), claimed by thread 0 when the current item's tiles are done (at_loop_end) or,
+// for an item that ends early, after it.  The counter only grows, so every workgroup exits after at
+// most items / gridDim.x + 1 tickets.
+template <class E, int D, int GC, bool UB, bool AP>
+__global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) {
+  __shared__ uint16_t s_parts[kQueueMaxBatch];  // partitions of sequence b
+  __shared__ uint16_t s_order[kQueueMaxBatch];  // sequences by partition count, descending
+  __shared__ int s_level[kQueueMaxLevels + 1];  // first item of each level; [levels] = item count
+  __shared__ int s_ticket;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int heads_per_seq = p.kv_heads * p.head_chunks;
+  const bool is64 = p.index_is64 != 0;
+  const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << p.bs_log2;
+  const int P = p.partition_tokens;
+
+  for (int i = tid; i < p.batch; i += kThreads) {
+    const int64_t c = index_value(load_raw_index(p.context_lengths, i, is64), is64);
+    const int64_t cc = c < max_ctx ? c : max_ctx;
+    s_parts[i] = static_cast<uint16_t>(cc <= 0 ? 1 : (cc + P - 1) / P);
+  }
+  __syncthreads();
+  // Stable rank by descending partition count.
+  for (int i = tid; i < p.batch; i += kThreads) {
+    const int mine = s_parts[i];
+    int pos = 0;
+    for (int o = 0; o < p.batch; ++o) {
+      const int other = s_parts[o];
+      pos += (other > mine || (other == mine && o < i)) ? 1 : 0;
+    }
+    s_order[pos] = static_cast<uint16_t>(i);
+  }
+  __syncthreads();
+  // Level k holds the sequences whose count exceeds k: a prefix of the order, found by bisection.
+  const int levels = s_parts[s_order[0]];
+  for (int k = tid; k < levels; k += kThreads) {
+    int lo = 0, hi = p.batch;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_parts[s_order[mid]] > k) lo = mid + 1; else hi = mid;
+    }
+    s_level[k + 1] = lo * heads_per_seq;
+  }
+  __syncthreads();
+  if (tid < kWave) {  // exclusive prefix over the levels: four per lane, then a wave scan
+    constexpr int PER = kQueueMaxLevels / kWave;
+    int v[PER];
+    int local = 0;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int k = lane * PER + e;
+      v[e] = k < levels ? s_level[k + 1] : 0;
+      local += v[e];
+    }
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int other = __shfl_up(incl, off);
+      if (lane >= off) incl += other;
+    }
+    int run = incl - local;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int k = lane * PER + e;
+      run += v[e];
+      if (k < levels) s_level[k + 1] = run;
+    }
+    if (lane == 0) s_level[0] = 0;
+  }
+  __syncthreads();
+  const int items = s_level[levels];
+
+  auto claim = [&]() { s_ticket = static_cast<int>(gridDim.x) + static_cast<int>(__hip_atomic_fetch_add(
+                                      p.queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)); };
+  int t = blockIdx.x;
+  while (t < items) {
+    // Level of item t: the last level starting at or before it.
+    int lo = 0, hi = levels - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_level[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int rem = t - s_level[lo];
+    const int b = __builtin_amdgcn_readfirstlane(s_order[rem / heads_per_seq]);
+    const int hslot = __builtin_amdgcn_readfirstlane(rem % heads_per_seq);
+    const int part = __builtin_amdgcn_readfirstlane(lo);
+    bool claimed = false;  // by thread 0
+    // The thread index passes through an empty asm statement each item, so nothing computed from it
+    // is hoisted out of this loop: per-lane offsets are rebuilt per item instead of holding registers
+    // through every item's epilogue (hoisted, they took the 128-dim GQA-4 form to one wave per SIMD).
+    int item_tid = tid;
+    __asm__ volatile("" : "+v"(item_tid));
+    partition_item<E, D, GC, true, UB, AP>(p, item_tid, b, hslot, part, [&]() __attribute__((always_inline)) {
+      if (tid == 0) {
+        claim();
+        claimed = true;
+      }
+    });
+    __syncthreads();
+    if (tid == 0 && !claimed) claim();
+    __syncthreads();
+    t = s_ticket;
+  }
+}
+
+// Zeroes the work-queue ticket counter in front of a queue launch (a kernel, not a memset, so the
+// pair can be captured in a graph).  An agent-scope store, like the tickets' atomics.
+__global__ void pa_queue_reset_kernel(uint32_t* queue) {
+  if (threadIdx.x == 0) __hip_atomic_store(queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host side.
 thread_local std::string g_last_error;
@@ -1104,7 +1251,8 @@ int64_t partitions_for(const Shape& s) {
   return (s.max_blocks * s.block_size + s.partition - 1) / s.partition;
 }
 
-// Workspace layout: partition accumulators (fp32, padded to 256 B), then partition (max, sum) pairs.
+// Workspace layout: a 256-byte header (word 0: the work-queue ticket counter), partition
+// accumulators (fp32, padded to 256 B), then partition (max, sum) pairs.
 size_t acc_bytes_for(const Shape& s) {
   const size_t records = static_cast<size_t>(s.batch) * s.query_heads * s.num_partitions;
   return (records * s.head_dim * sizeof(float) + 255) & ~size_t{255};
@@ -1113,7 +1261,14 @@ size_t acc_bytes_for(const Shape& s) {
 size_t workspace_for(const Shape& s) {
   if (s.num_partitions <= 1) return 0;
   const size_t records = static_cast<size_t>(s.batch) * s.query_heads * s.num_partitions;
-  return acc_bytes_for(s) + records * 2 * sizeof(float);
+  return kQueueHeaderBytes + acc_bytes_for(s) + records * 2 * sizeof(float);
+}
+
+// The work-queue schedule needs the workspace header (split-K shapes) and an item map that fits in
+// the queue kernel's LDS; the VALU variant is not built for it.
+bool queue_eligible(const Shape& s, int variant) {
+  return variant == RK_PA_VARIANT_MFMA && s.num_partitions > 1 && s.num_partitions <= kQueueMaxLevels &&
+         s.batch <= kQueueMaxBatch;
 }
 
 // Arrival counters of the fused launch: one 32-bit word per (sequence, KV head, head chunk).
@@ -1123,39 +1278,90 @@ int64_t counter_words_for(int64_t batch, int64_t query_heads, int64_t kv_heads) 
   return batch * kv_heads * ((group + gc - 1) / gc);
 }
 
-template <class E, int D, int GC, bool QK_MFMA, bool AP>
-void launch_partition_ub(const Params& prm, int64_t grid, hipStream_t stream) {
-  if (prm.bs_log2 >= 4) {
-    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, true, AP>),
-                       dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, prm);
-  } else {
-    hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, false, AP>),
-                       dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, prm);
+// Schedule requests (the RK_PA_SCHEDULE_* bits of the variant argument).
+constexpr int kScheduleAuto = 0;
+constexpr int kScheduleGrid = 1;
+constexpr int kScheduleQueue = 2;
+
+// Workgroups of one queue-kernel instantiation the current device holds at once (resident
+// workgroups per CU, from the kernel's registers and LDS, times the CU count).
+struct Residency {
+  hipError_t err;
+  int per_cu;
+};
+template <class E, int D, int GC, bool UB, bool AP>
+hipError_t queue_capacity(int64_t* capacity) {
+  static const Residency r = [] {
+    Residency out{hipSuccess, 0};
+    out.err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &out.per_cu, reinterpret_cast<const void*>(&pa_partition_queue_kernel<E, D, GC, UB, AP>), kThreads, 0);
+    return out;
+  }();
+  if (r.err != hipSuccess) return r.err;
+  constexpr int kMaxDevices = 256;
+  static std::atomic<int> cus[kMaxDevices];
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return err;
+  int n = device >= 0 && device < kMaxDevices ? cus[device].load(std::memory_order_relaxed) : 0;
+  if (n == 0) {
+    err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return err;
+    if (device >= 0 && device < kMaxDevices) cus[device].store(n, std::memory_order_relaxed);
   }
+  *capacity = static_cast<int64_t>(r.per_cu > 0 ? r.per_cu : 1) * n;
+  return hipSuccess;
 }
 
-template <class E, int D, int GC>
-hipError_t launch_partition(const Params& prm, int variant, int64_t grid, hipStream_t stream) {
-  if (prm.new_k != nullptr)
-    launch_partition_ub<E, D, GC, true, true>(prm, grid, stream);  // validated: MFMA variant
-  else if (variant == RK_PA_VARIANT_MFMA)
-    launch_partition_ub<E, D, GC, true, false>(prm, grid, stream);
-  else
-    launch_partition_ub<E, D, GC, false, false>(prm, grid, stream);
+// The partition launch for `items` work items.  With a queue counter (prm.queue: a split-K shape
+// whose item map fits the queue kernel) the work-queue schedule runs when asked for, or, by default,
+// when the items exceed what the device holds at once; otherwise one workgroup per item.
+template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP>
+hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedule, hipStream_t stream) {
+  if constexpr (QK_MFMA) {
+    if (prm.queue != nullptr) {
+      int64_t capacity = 0;
+      const hipError_t err = queue_capacity<E, D, GC, UB, AP>(&capacity);
+      if (err != hipSuccess) return err;
+      if (schedule == kScheduleQueue || items > capacity) {
+        hipLaunchKernelGGL(pa_queue_reset_kernel, dim3(1), dim3(kWave), 0, stream, prm.queue);
+        const int64_t grid = items < capacity ? items : capacity;
+        hipLaunchKernelGGL((pa_partition_queue_kernel<E, D, GC, UB, AP>), dim3(static_cast<uint32_t>(grid)),
+                           dim3(kThreads), 0, stream, prm);
+        return hipGetLastError();
+      }
+    }
+  }
+  hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, UB, AP>), dim3(static_cast<uint32_t>(items)),
+                     dim3(kThreads), 0, stream, prm);
   return hipGetLastError();
 }
 
+template <class E, int D, int GC, bool QK_MFMA, bool AP>
+hipError_t launch_partition_ub(const Params& prm, int64_t items, int schedule, hipStream_t stream) {
+  if (prm.bs_log2 >= 4) return launch_partition_kernel<E, D, GC, QK_MFMA, true, AP>(prm, items, schedule, stream);
+  return launch_partition_kernel<E, D, GC, QK_MFMA, false, AP>(prm, items, schedule, stream);
+}
+
+template <class E, int D, int GC>
+hipError_t launch_partition(const Params& prm, int variant, int64_t items, int schedule, hipStream_t stream) {
+  if (prm.new_k != nullptr)
+    return launch_partition_ub<E, D, GC, true, true>(prm, items, schedule, stream);  // validated: MFMA
+  if (variant == RK_PA_VARIANT_MFMA) return launch_partition_ub<E, D, GC, true, false>(prm, items, schedule, stream);
+  return launch_partition_ub<E, D, GC, false, false>(prm, items, schedule, stream);
+}
+
 template <class E, int D>
-hipError_t launch_all(const Params& prm, int gc, int variant, int64_t grid, bool partitions,
+hipError_t launch_all(const Params& prm, int gc, int variant, int64_t grid, int schedule, bool partitions,
                       bool reduce, hipStream_t stream) {
   hipError_t err = hipSuccess;
   if (partitions) {
     if (gc == 1)
-      err = launch_partition<E, D, 1>(prm, variant, grid, stream);
+      err = launch_partition<E, D, 1>(prm, variant, grid, schedule, stream);
     else if (gc == 2)
-      err = launch_partition<E, D, 2>(prm, variant, grid, stream);
+      err = launch_partition<E, D, 2>(prm, variant, grid, schedule, stream);
     else
-      err = launch_partition<E, D, 4>(prm, variant, grid, stream);
+      err = launch_partition<E, D, 4>(prm, variant, grid, schedule, stream);
   }
   if (err != hipSuccess || !reduce) return err;
   const int64_t rows = static_cast<int64_t>(prm.batch) * prm.query_heads;
@@ -1166,11 +1372,11 @@ hipError_t launch_all(const Params& prm, int gc, int variant, int64_t grid, bool
 }
 
 template <class E>
-hipError_t launch_dtype(const Params& prm, int64_t head_dim, int gc, int variant, int64_t grid,
+hipError_t launch_dtype(const Params& prm, int64_t head_dim, int gc, int variant, int64_t grid, int schedule,
                         bool partitions, bool reduce, hipStream_t stream) {
-  if (head_dim == 64) return launch_all<E, 64>(prm, gc, variant, grid, partitions, reduce, stream);
-  if (head_dim == 128) return launch_all<E, 128>(prm, gc, variant, grid, partitions, reduce, stream);
-  return launch_all<E, 256>(prm, gc, variant, grid, partitions, reduce, stream);
+  if (head_dim == 64) return launch_all<E, 64>(prm, gc, variant, grid, schedule, partitions, reduce, stream);
+  if (head_dim == 128) return launch_all<E, 128>(prm, gc, variant, grid, schedule, partitions, reduce, stream);
+  return launch_all<E, 256>(prm, gc, variant, grid, schedule, partitions, reduce, stream);
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
@@ -1265,7 +1471,7 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   const bool append = (phases & kPhaseAppend) != 0;
   if (append && (!new_key || !new_value))
     return fail(RK_ERR_INVALID_ARGUMENT, "new_key and new_value must not be NULL");
-  if (append && variant != RK_PA_VARIANT_MFMA)
+  if (append && (variant & 0xFF) != RK_PA_VARIANT_MFMA)
     return fail(RK_ERR_UNSUPPORTED, "append-and-decode is built for RK_PA_VARIANT_MFMA only");
   if (append && (!aligned16(new_key) || !aligned16(new_value)))
     return fail(RK_ERR_UNSUPPORTED, "new_key and new_value must be 16-byte aligned");
@@ -1273,6 +1479,13 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
     return fail(RK_ERR_INVALID_ARGUMENT, "dtype must be RK_DTYPE_FP16 or RK_DTYPE_BF16");
   if (index_dtype != RK_INDEX_INT32 && index_dtype != RK_INDEX_INT64)
     return fail(RK_ERR_INVALID_ARGUMENT, "index_dtype must be RK_INDEX_INT32 or RK_INDEX_INT64");
+  if ((variant & ~(RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE | 0xFF)) != 0 ||
+      (variant & (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE)) == (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE))
+    return fail(RK_ERR_INVALID_ARGUMENT, "unknown kernel variant %d", variant);
+  const int schedule = (variant & RK_PA_SCHEDULE_QUEUE) != 0   ? kScheduleQueue
+                       : (variant & RK_PA_SCHEDULE_GRID) != 0 ? kScheduleGrid
+                                                               : kScheduleAuto;
+  variant &= 0xFF;
   if (variant != RK_PA_VARIANT_MFMA && variant != RK_PA_VARIANT_VALU)
     return fail(RK_ERR_INVALID_ARGUMENT, "unknown kernel variant %d", variant);
   if (!(scale > 0.0f) || !isfinite(scale))
@@ -1330,9 +1543,17 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.context_lengths = context_lengths;
   prm.out = static_cast<uint16_t*>(output);
   if (need > 0) {
-    prm.ws_acc = static_cast<float*>(workspace);
-    prm.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes_for(s));
+    char* records = static_cast<char*>(workspace) + kQueueHeaderBytes;
+    prm.ws_acc = reinterpret_cast<float*>(records);
+    prm.ws_ml = reinterpret_cast<float*>(records + acc_bytes_for(s));
   }
+  const bool partitions = (phases & (kPhasePartitions | kPhaseFused)) != 0;
+  const bool queue = partitions && schedule != kScheduleGrid && queue_eligible(s, variant);
+  if (partitions && schedule == kScheduleQueue && !queue)
+    return fail(RK_ERR_UNSUPPORTED,
+                "the work-queue schedule needs the MFMA variant, more than one partition per sequence "
+                "(at most %d) and at most %d sequences", kQueueMaxLevels, kQueueMaxBatch);
+  if (queue) prm.queue = static_cast<uint32_t*>(workspace);
   prm.counters = fused ? counters : nullptr;
   if (append) {
     prm.new_k = static_cast<const uint16_t*>(new_key);
@@ -1355,13 +1576,12 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.index_is64 = index_dtype == RK_INDEX_INT64 ? 1 : 0;
   prm.scale_log2e = scale * kLog2e;
 
-  const bool partitions = (phases & (kPhasePartitions | kPhaseFused)) != 0;
   const bool reduce = !fused && (phases & kPhaseReduce) != 0 && s.num_partitions > 1;
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const hipError_t err =
       dtype == RK_DTYPE_BF16
-          ? launch_dtype<Bf16>(prm, head_dim, gc, variant, grid, partitions, reduce, hs)
-          : launch_dtype<Fp16>(prm, head_dim, gc, variant, grid, partitions, reduce, hs);
+          ? launch_dtype<Bf16>(prm, head_dim, gc, variant, grid, schedule, partitions, reduce, hs)
+          : launch_dtype<Fp16>(prm, head_dim, gc, variant, grid, schedule, partitions, reduce, hs);
   if (err != hipSuccess)
     return fail(RK_ERR_LAUNCH, "paged attention launch failed: %s", hipGetErrorString(err));
   return RK_OK;

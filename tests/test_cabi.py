@@ -71,14 +71,18 @@ def test_status_codes_match_header():
         assert getattr(cabi, name) == value, name
     assert cabi.VARIANTS == {"mfma": int(re.search(r"RK_PA_VARIANT_MFMA (\d+)", text).group(1)),
                              "valu": int(re.search(r"RK_PA_VARIANT_VALU (\d+)", text).group(1))}
+    assert cabi.SCHEDULES == {"auto": 0, "grid": int(re.search(r"RK_PA_SCHEDULE_GRID (0x[0-9a-f]+)", text).group(1), 16),
+                              "queue": int(re.search(r"RK_PA_SCHEDULE_QUEUE (0x[0-9a-f]+)", text).group(1), 16)}
 
 
 def expected_workspace(batch, hq, d, bs, mb, partition):
+    """256-byte work-queue header, accumulator records padded to 256 B, then (max, sum) pairs."""
+
     parts = -(-(mb * bs) // partition)
     if parts <= 1:
         return 0
     records = batch * hq * parts
-    return ((records * d * 4 + 255) // 256) * 256 + records * 2 * 4
+    return 256 + ((records * d * 4 + 255) // 256) * 256 + records * 2 * 4
 
 
 @pytest.mark.parametrize("shape", [(128, 32, 128, 16, 1024, 2048), (8, 32, 128, 16, 64, 64), (1, 32, 128, 16, 8, 128),
@@ -132,6 +136,17 @@ def call(lib, **overrides):
         (dict(max_blocks=64, partition_tokens=64), cabi.RK_ERR_WORKSPACE, "workspace of"),
         (dict(max_blocks=64, partition_tokens=64, workspace=4096 + 64, workspace_bytes=1 << 20), cabi.RK_ERR_WORKSPACE,
          "256-byte aligned"),
+        # Schedule bits: both at once, or an unknown bit, are invalid; the queue needs the MFMA variant,
+        # a split-K shape (several partitions), at most 256 partitions and at most 1024 sequences.
+        (dict(variant=0x300), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        (dict(variant=0x400), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        (dict(variant=0x201, max_blocks=64, workspace=1 << 20, workspace_bytes=1 << 20), cabi.RK_ERR_UNSUPPORTED,
+         "work-queue schedule"),
+        (dict(variant=0x200), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
+        (dict(variant=0x200, max_blocks=1024, partition_tokens=16, workspace=1 << 20, workspace_bytes=1 << 30),
+         cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
+        (dict(variant=0x200, batch=1025, max_blocks=64, workspace=1 << 20, workspace_bytes=1 << 30),
+         cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
     ],
 )
 @cpu_only

@@ -1,0 +1,194 @@
+"""Work-queue schedule of the partition kernel (RK_PA_SCHEDULE_QUEUE) against the one-workgroup-per-item
+grid (RK_PA_SCHEDULE_GRID).
+
+Both schedules run the same per-item code, so outputs must be bit-identical (compared as raw bits,
+NaN rows of empty contexts included); the queue form is also checked against the float64 oracle.
+The cases cover what the queue's item map is built from: ragged contexts whose partition counts
+differ per sequence, empty and negative contexts (one NaN item), contexts past the table, int32 and
+int64 indices, head chunks of 1, 2 and 4 query heads (and two chunks per KV head), block sizes below
+a tile, every head_dim, the fused, two-launch, phase-split, append and allocation-free entries, a
+garbage-filled workspace header, repeated calls and a smaller call after a larger one.
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from _helpers import announce, assert_within, make_case, oracle64, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def same_bits(a, b) -> bool:
+    import torch
+
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def ragged_contexts(batch, limit, seed):
+    """Context lengths in [1, limit] with an empty, a negative and a past-the-table length mixed in."""
+
+    import random
+
+    rng = random.Random(seed)
+    contexts = [rng.randint(1, limit) for _ in range(batch)]
+    contexts[1] = 0
+    contexts[batch // 2] = -3
+    contexts[-2] = limit + 77  # clamped to the table
+    contexts[-1] = limit
+    return contexts
+
+
+# (query_heads, kv_heads, head_dim, block_size, dtype, index_dtype, partition): head chunks of 4, 1,
+# 2 and two chunks of 4; blocks of 16, 32, 8 and 1 tokens; every head_dim.
+SHAPES = [
+    (32, 8, 128, 16, "bf16", "int32", 128),
+    (16, 16, 64, 32, "bf16", "int64", 64),
+    (16, 8, 128, 8, "fp16", "int64", 128),
+    (64, 8, 128, 1, "bf16", "int32", 64),
+    (32, 8, 256, 16, "fp16", "int32", 128),
+]
+
+
+def shape_id(shape):
+    hq, hkv, d, bs, dtype, index, partition = shape
+    return f"h{hq}x{hkv}-d{d}-bs{bs}-{dtype}-{index}-p{partition}"
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=shape_id)
+def test_queue_matches_grid_and_oracle(gpu, palib, shape):
+    import torch
+
+    hq, hkv, d, bs, dtype, index, partition = shape
+    batch, limit = 40, 1000
+    contexts = ragged_contexts(batch, limit, seed=d + bs)
+    max_blocks = -(-limit // bs)
+    case = make_case(torch, batch=batch, query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bs,
+                     contexts=contexts, max_blocks=max_blocks, dtype=dtype, index_dtype=index, seed=11)
+    dev = to_device(case, gpu)
+    args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    announce(f"queue vs grid {shape_id(shape)} batch {batch}")
+    grid = palib.decode(*args, partition_tokens=partition, schedule="grid")
+    queue = palib.decode(*args, partition_tokens=partition, schedule="queue")
+    auto = palib.decode(*args, partition_tokens=partition)
+    torch.cuda.synchronize()
+    assert same_bits(queue, grid)
+    assert same_bits(auto, grid)
+    assert_within(queue, oracle64(case), dtype, f"queue {shape_id(shape)}")
+
+
+@pytest.mark.parametrize("phase", ["fused", "split"])
+def test_queue_in_every_launch_form(gpu, palib, phase):
+    import torch
+
+    batch, limit, bs, partition = 48, 2048, 16, 128
+    case = make_case(torch, batch=batch, query_heads=32, kv_heads=8, head_dim=128, block_size=bs,
+                     contexts=ragged_contexts(batch, limit, seed=3), max_blocks=limit // bs, seed=5)
+    dev = to_device(case, gpu)
+    args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    announce(f"queue launch form {phase}")
+    expected = palib.decode(*args, partition_tokens=partition, schedule="grid")
+    if phase == "fused":
+        counters = torch.zeros(palib.counter_words(batch, 32, 8), dtype=torch.int32, device=gpu)
+        got = palib.decode(*args, partition_tokens=partition, phase="fused", counters=counters, schedule="queue")
+        again = palib.decode(*args, partition_tokens=partition, phase="fused", counters=counters, schedule="queue")
+        torch.cuda.synchronize()
+        assert same_bits(again, got)
+        assert int(counters.abs().sum()) == 0  # every arrival counter left zero
+        reference = palib.decode(*args, partition_tokens=partition, phase="fused", counters=counters,
+                                 schedule="grid")
+        torch.cuda.synchronize()
+        assert same_bits(got, reference)
+    else:
+        need = palib.workspace_bytes(batch, 32, 128, bs, limit // bs, partition)
+        ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+        out = torch.empty_like(dev["query"])
+        palib.decode(*args, partition_tokens=partition, out=out, workspace=ws, phase="partitions", schedule="queue")
+        palib.decode(*args, partition_tokens=partition, out=out, workspace=ws, phase="reduce")
+        torch.cuda.synchronize()
+        assert same_bits(out, expected)
+
+
+def test_garbage_header_repeated_and_shrinking_calls(gpu, palib):
+    """The ticket counter is zeroed in front of every queue launch: a workspace full of 0xFF, repeated
+    calls on it, and a smaller call after a larger one all give the grid schedule's outputs."""
+
+    import torch
+
+    bs, partition, limit = 16, 128, 1536
+    big = make_case(torch, batch=64, query_heads=32, kv_heads=8, head_dim=128, block_size=bs,
+                    contexts=ragged_contexts(64, limit, seed=8), max_blocks=limit // bs, seed=2)
+    small = make_case(torch, batch=6, query_heads=32, kv_heads=8, head_dim=128, block_size=bs,
+                      contexts=ragged_contexts(6, limit, seed=9), max_blocks=limit // bs, seed=4)
+    need = palib.workspace_bytes(64, 32, 128, bs, limit // bs, partition)
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=gpu)
+    for name, case in (("big", big), ("small", small), ("big", big)):
+        dev = to_device(case, gpu)
+        args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+        announce(f"queue reuse {name}")
+        expected = palib.decode(*args, partition_tokens=partition, schedule="grid")
+        for _ in range(3):
+            got = palib.decode(*args, partition_tokens=partition, workspace=ws, schedule="queue")
+            torch.cuda.synchronize()
+            assert same_bits(got, expected)
+
+
+def test_append_and_noalloc_on_the_queue(gpu, palib, kvlib):
+    import torch
+
+    from test_gpu_append_decode import new_rows, new_token_slots
+
+    batch, limit, bs, partition = 40, 1024, 16, 64
+    case = make_case(torch, batch=batch, query_heads=32, kv_heads=8, head_dim=128, block_size=bs,
+                     contexts=ragged_contexts(batch, limit, seed=21), max_blocks=limit // bs, seed=6)
+    dev = to_device(case, gpu)
+    q, kc, vc, bt, cl = (dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths"))
+    announce("queue append-and-decode")
+    nk, nv = new_rows(torch, q, 8, seed=13)
+    ref_k, ref_v = kc.clone(), vc.clone()
+    kvlib.append(nk, nv, ref_k, ref_v, new_token_slots(torch, bt, cl, bs))
+    expected = palib.decode(q, ref_k, ref_v, bt, cl, partition_tokens=partition, schedule="grid")
+    got_k, got_v = kc.clone(), vc.clone()
+    got = palib.decode(q, got_k, got_v, bt, cl, partition_tokens=partition, new_key=nk, new_value=nv,
+                       schedule="queue")
+    torch.cuda.synchronize()
+    assert same_bits(got, expected)
+    assert torch.equal(got_k, ref_k) and torch.equal(got_v, ref_v)
+
+    announce("queue allocation-free decode")
+    plain = palib.decode(q, kc, vc, bt, cl, partition_tokens=partition, schedule="grid")
+    out = torch.empty_like(q)
+    palib.decode_noalloc(q, kc, vc, bt, cl, out=out, partition_tokens=partition, schedule="queue")
+    torch.cuda.synchronize()
+    assert same_bits(out, plain)
+
+
+def test_queue_with_fewer_items_than_workgroups(gpu, palib):
+    """Forced onto a grid that fits the device at once: the workgroups past the item count exit."""
+
+    import torch
+
+    case = make_case(torch, batch=3, query_heads=8, kv_heads=2, head_dim=128, block_size=16,
+                     contexts=[300, 0, 129], max_blocks=20, seed=1)
+    dev = to_device(case, gpu)
+    args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    announce("queue small grid")
+    grid = palib.decode(*args, partition_tokens=64, schedule="grid")
+    queue = palib.decode(*args, partition_tokens=64, schedule="queue")
+    torch.cuda.synchronize()
+    assert same_bits(queue, grid)
+    assert_within(queue, oracle64(case), "bf16", "queue small grid")
+
+
+def test_ragged_b128_workload_schedules_agree(gpu, palib, c5_case):
+    """The 128-sequence ragged workload (8192 work items) takes the queue by default."""
+
+    import torch
+
+    dev = c5_case["gpu"]
+    args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    announce("queue b128 ragged P=2048")
+    grid = palib.decode(*args, partition_tokens=2048, schedule="grid")
+    auto = palib.decode(*args, partition_tokens=2048)
+    torch.cuda.synchronize()
+    assert same_bits(auto, grid)

@@ -4,7 +4,10 @@
 One step = one decode call over the whole batch of the workload, inputs resident in HBM, in the form
 the workload's dispatch entry selects (launch.merge): "reduce" -- the partition kernel followed by the
 partition-reduce kernel -- or "fused" -- the partition kernel alone, its last workgroup per sequence
-and head slot merging the partition records.  --merge overrides the entry.  Default workload: 128 sequences, 32 query / 8 KV heads, head_dim
+and head slot merging the partition records.  --merge overrides the entry.  The library runs the
+partition kernel on the work-queue schedule when the call's work items exceed the workgroups the GPU
+holds at once (config.schedule; the kernel is then pa_partition_queue_kernel, launched behind a
+one-thread kernel that zeroes its ticket counter), else one workgroup per work item.  Default workload: 128 sequences, 32 query / 8 KV heads, head_dim
 128, block 16, bf16, context lengths ~ U[1024, 16384] (seeded), about 4.8 GB of K/V per call -- 18x
 the 256 MB last-level cache, so every call streams from HBM.
 
@@ -15,7 +18,7 @@ Prints one JSON line:
   roofline         the partition kernel against the 8 TB/s HBM peak: achieved = KV bytes / its
                    average duration, from HIP events recorded on the launch stream around K
                    back-to-back launches of that kernel alone (in the fused form the call is that
-                   one kernel); traffic = measured HBM bytes per launch from the committed
+                   one kernel, plus the queue's counter reset on the work-queue schedule); traffic = measured HBM bytes per launch from the committed
                    rocprofv3 counter summary for this exact configuration (null when there is none)
   kernels_us       per-launch averages of the reduce form's two kernels; us_per_call_reduce and
                    us_per_call_fused time both whole-call forms (omitted with --no-breakdown, which
@@ -589,7 +592,7 @@ def main(argv=None) -> int:
     variant = args.variant or decision["selected"].split("/", 1)[1].split("_", 1)[1]  # native/decode_<variant>
     partition = args.partition or int(decision["launch"]["partition_tokens"])
     merge = args.merge or str(decision["launch"]["merge"])
-    if merge == "auto":  # the broad region's choice: fused below 4096 workgroups
+    if merge == "auto":  # the broad region's choice: fused
         merge = "fused"
     kv_bytes = data["kv_bytes"]
     cache_bytes = data["key_cache"].numel() * 2 * 2
@@ -609,6 +612,8 @@ def main(argv=None) -> int:
     counters = torch.zeros(lib.counter_words(batch, hq, hkv), dtype=torch.int32, device=device)
     stream = torch.cuda.current_stream(device)
     headline = "fused" if merge == "fused" else "all"
+    schedule = lib.schedule(batch, hq, hkv, d, bs, mb, w.dtype, partition, variant)
+    partition_kernel = "pa_partition_queue_kernel" if schedule == "queue" else "pa_partition_kernel"
 
     # Every launch's ctypes arguments are built once, so a timed loop makes one foreign call per
     # launch: on the small workloads the wrapper's Python would otherwise outrun the GPU time.
@@ -746,6 +751,7 @@ def main(argv=None) -> int:
             "context": list(w.context) if w.ragged else w.context, "seed": data["seed"],
             "entrypoint": f"decode_{variant}", "partition_tokens": partition, "kv_copies_rotated": copies,
             "merge": merge,
+            "schedule": schedule,
             "arch": arch,
         },
         "us_per_call": round(us_per_call, 2),
@@ -753,7 +759,7 @@ def main(argv=None) -> int:
         "pct_hbm_peak": round(gbps / HBM_PEAK_GBPS * 100, 2),
         "kv_bytes_per_call": kv_bytes,
         "kernels_us": None if part_avg is None else {
-            "pa_partition_kernel": round(part_avg, 2),
+            partition_kernel: round(part_avg, 2),
             "pa_reduce_kernel": None if red_avg is None else round(red_avg, 2)},
         "us_per_call_reduce": round(forms["reduce"], 2) if "reduce" in forms else None,
         "us_per_call_fused": round(forms["fused"], 2) if "fused" in forms else None,

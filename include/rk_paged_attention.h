@@ -23,6 +23,7 @@
  *                              (benchmarks/kv_cache/native_kv_cache.hip:22-51, one token per
  *                              sequence at position context_length - 1) followed by rk_pa_decode, in
  *                              the decode's own launch.
+ *   rk_pa_decode_schedule  -> no reference counterpart: which partition-kernel schedule a call runs.
  *   rk_pa_last_error, rk_pa_version
  *                           -> error text that TORCH_CHECK carried in the reference
  *                              (native_paged_attention.hip:199-219,239-240).
@@ -87,6 +88,16 @@ extern "C" {
  */
 #define RK_PA_SCHEDULE_GRID 0x100
 #define RK_PA_SCHEDULE_QUEUE 0x200
+
+/*
+ * The schedule (RK_PA_SCHEDULE_GRID or RK_PA_SCHEDULE_QUEUE) that rk_pa_decode, its phase entries,
+ * rk_pa_decode_fused and rk_pa_decode_noalloc run for these arguments on the current device (no
+ * reference counterpart).  The index dtype does not enter the choice.  Launches nothing; the first
+ * query of a kernel configuration reads its occupancy from the runtime.
+ */
+int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                          int64_t block_size, int64_t max_blocks_per_sequence, int dtype,
+                          int64_t partition_tokens, int variant, int* schedule);
 
 /*
  * Bytes of device workspace rk_pa_decode needs for this shape and partition size: a 256-byte

@@ -54,6 +54,11 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # Every atomic in these kernels is issued by a single lane.  The atomic optimizer would rewrite
+    # each into its lane-combining form, which reads the result back at once (a full memory-counter
+    # wait) instead of where it is used.
+    "-mllvm",
+    "-amdgpu-atomic-optimizer-strategy=None",
     f"-ffile-prefix-map={REPO_ROOT}=.",
 ]
 

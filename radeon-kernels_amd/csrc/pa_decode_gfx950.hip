@@ -444,11 +444,12 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
 //
 // partition_item is one work item (sequence b, head slot = KV head * head_chunks + head chunk,
 // partition part) run by the whole workgroup (tid = threadIdx.x); the two kernels below differ only
-// in how they hand out work items.  at_loop_end() runs in every wave once the item's tiles are done,
-// before its epilogue.
-template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP, class LoopEnd>
+// in how they hand out work items.  at_epilogue() runs in every wave once the item's loads have all
+// landed, at the start of its epilogue (not for an item that ends early: an empty context or a
+// partition past it); memory operations it issues are waited for only where their results are used.
+template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP, class Epilogue>
 __device__ __attribute__((always_inline)) inline void partition_item(const Params& p, const int tid, int b, int hslot,
-                                                                     int part, LoopEnd&& at_loop_end) {
+                                                                     int part, Epilogue&& at_epilogue) {
   static_assert(!AP || QK_MFMA, "append-and-decode is built for the MFMA variant");
   constexpr int KSTEPS = D / 32;       // MFMA k-steps; also DMA instructions per K tile
   constexpr int VEC = D / 16;          // elements of a token row per lane (row = 16 lanes)
@@ -967,7 +968,6 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
     });
   }
 
-  at_loop_end();
   // Wave totals: sum the four lane groups (they hold disjoint tokens, identical maxima).
   l_own = sum_xor16(l_own);
   l_own = sum_xor32(l_own);
@@ -982,6 +982,7 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   // and every wave must be done reading its K slots.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  at_epilogue();
   if (g == 0) {
 #pragma unroll
     for (int h = 0; h < GC; ++h)
@@ -1067,26 +1068,33 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 // per-workgroup timeline of the 128-sequence ragged workload showed 2-12 us between one
 // workgroup's end and the next one's start on the same CU) and a launch plus a context-length load
 // for every item past its sequence's context (3672 of its 8192 items, about 4 us each); here only
-// items with tokens are scheduled, and a workgroup's next item is claimed while its current one
-// finishes.
+// items with tokens are scheduled.
 //
-// Item map, built by every workgroup from the context lengths alone, so all agree on it: level k
-// holds partition k of every sequence with more than k partitions (a context <= 0 counts one
-// partition, whose item writes the NaN row), with the sequences ordered by partition count,
-// largest first (ties by index), and the head slot fastest.  Items are numbered level by level.
-// Level order keeps the grid schedule's partition-slowest walk; the count order inside a level puts
-// the sequences with the most work left first.
+// Item map, built by every workgroup from the context lengths alone, so all agree on it.  A
+// sequence with c > 0 tokens (clamped to the table) has f = c / P full partitions and, when P does
+// not divide c, one partial partition of c % P tokens; a context <= 0 has one partial partition of
+// no tokens (its item writes the NaN row).  Items are numbered largest first: the full partitions
+// level by level (level k: partition k of every sequence with more than k full partitions, the
+// sequences by full count, largest first, ties by index), then the partial partitions by size,
+// largest first (ties by index); the head slot is fastest throughout.  The smallest items come last,
+// so the workgroups run out of work at nearly the same time.
 //
 // Workgroup w runs item w first; every further item comes from the ticket counter
-// (gridDim.x + ticket), claimed by thread 0 when the current item's tiles are done (at_loop_end) or,
-// for an item that ends early, after it.  The counter only grows, so every workgroup exits after at
-// most items / gridDim.x + 1 tickets.
+// (gridDim.x + ticket).  Thread 0 claims its workgroup's next ticket at the start of the current
+// item's epilogue, decodes it once the epilogue is done and publishes (ticket, sequence, head slot,
+// partition) in LDS for the next item.  Claiming at the start of an item instead (one item ahead)
+// measured 3% slower on the 128-sequence ragged workload; this order of items measured 1.5%
+// faster than partition-major levels over all partitions.  The counter only grows, so every
+// workgroup exits after at most items / gridDim.x + 1 tickets.
 template <class E, int D, int GC, bool UB, bool AP>
 __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) {
-  __shared__ uint16_t s_parts[kQueueMaxBatch];  // partitions of sequence b
-  __shared__ uint16_t s_order[kQueueMaxBatch];  // sequences by partition count, descending
-  __shared__ int s_level[kQueueMaxLevels + 1];  // first item of each level; [levels] = item count
-  __shared__ int s_ticket;
+  __shared__ uint16_t s_full[kQueueMaxBatch];        // full partitions of sequence b
+  __shared__ int16_t s_partial[kQueueMaxBatch];      // tokens of its partial partition, -1: none
+  __shared__ uint16_t s_full_order[kQueueMaxBatch];  // sequences by full count, descending
+  __shared__ uint16_t s_part_order[kQueueMaxBatch];  // sequences with a partial, by its size, descending
+  __shared__ int s_level[kQueueMaxLevels + 1];       // first item of each full level; [levels] = full items
+  __shared__ int s_partials;
+  __shared__ int s_next[2][4];  // ticket, sequence, head slot, partition; by item parity
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int heads_per_seq = p.kv_heads * p.head_chunks;
@@ -1094,30 +1102,40 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
   const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << p.bs_log2;
   const int P = p.partition_tokens;
 
+  if (tid == 0) s_partials = 0;
   for (int i = tid; i < p.batch; i += kThreads) {
     const int64_t c = index_value(load_raw_index(p.context_lengths, i, is64), is64);
-    const int64_t cc = c < max_ctx ? c : max_ctx;
-    s_parts[i] = static_cast<uint16_t>(cc <= 0 ? 1 : (cc + P - 1) / P);
+    const int cc = static_cast<int>(c < max_ctx ? c : max_ctx);
+    s_full[i] = static_cast<uint16_t>(cc <= 0 ? 0 : cc / P);
+    s_partial[i] = static_cast<int16_t>(cc <= 0 ? 0 : (cc % P != 0 ? cc % P : -1));
   }
   __syncthreads();
-  // Stable rank by descending partition count.
+  // Stable ranks: by full count, and (sequences with a partial) by partial size, both descending.
+  int partials = 0;
   for (int i = tid; i < p.batch; i += kThreads) {
-    const int mine = s_parts[i];
-    int pos = 0;
+    const int full = s_full[i], part_size = s_partial[i];
+    int full_pos = 0, part_pos = 0;
     for (int o = 0; o < p.batch; ++o) {
-      const int other = s_parts[o];
-      pos += (other > mine || (other == mine && o < i)) ? 1 : 0;
+      const int other_full = s_full[o], other_part = s_partial[o];
+      full_pos += (other_full > full || (other_full == full && o < i)) ? 1 : 0;
+      part_pos += (other_part > part_size || (other_part == part_size && o < i)) ? 1 : 0;
     }
-    s_order[pos] = static_cast<uint16_t>(i);
+    s_full_order[full_pos] = static_cast<uint16_t>(i);
+    if (part_size >= 0) {
+      s_part_order[part_pos] = static_cast<uint16_t>(i);
+      ++partials;
+    }
   }
+  if (partials > 0) atomicAdd(&s_partials, partials);
   __syncthreads();
-  // Level k holds the sequences whose count exceeds k: a prefix of the order, found by bisection.
-  const int levels = s_parts[s_order[0]];
+  // Full level k holds the sequences whose full count exceeds k: a prefix of the order, found by
+  // bisection.
+  const int levels = s_full[s_full_order[0]];
   for (int k = tid; k < levels; k += kThreads) {
     int lo = 0, hi = p.batch;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (s_parts[s_order[mid]] > k) lo = mid + 1; else hi = mid;
+      if (s_full[s_full_order[mid]] > k) lo = mid + 1; else hi = mid;
     }
     s_level[k + 1] = lo * heads_per_seq;
   }
@@ -1148,23 +1166,52 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
     if (lane == 0) s_level[0] = 0;
   }
   __syncthreads();
-  const int items = s_level[levels];
+  const int full_items = __builtin_amdgcn_readfirstlane(s_level[levels]);
+  const int items = full_items + __builtin_amdgcn_readfirstlane(s_partials) * heads_per_seq;
 
-  auto claim = [&]() { s_ticket = static_cast<int>(gridDim.x) + static_cast<int>(__hip_atomic_fetch_add(
-                                      p.queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)); };
-  int t = blockIdx.x;
-  while (t < items) {
-    // Level of item t: the last level starting at or before it.
-    int lo = 0, hi = levels - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_level[mid] <= t) lo = mid; else hi = mid - 1;
+  // Thread 0: item t -> s_next[slot].
+  auto publish = [&](int slot, int t) {
+    int b = 0, hslot = 0, part = 0;
+    if (t < full_items) {
+      int lo = 0, hi = levels - 1;  // the last level starting at or before t
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_level[mid] <= t) lo = mid; else hi = mid - 1;
+      }
+      const int rem = t - s_level[lo];
+      b = s_full_order[rem / heads_per_seq];
+      hslot = rem % heads_per_seq;
+      part = lo;
+    } else if (t < items) {
+      const int rem = t - full_items;
+      b = s_part_order[rem / heads_per_seq];
+      hslot = rem % heads_per_seq;
+      part = s_full[b];
     }
-    const int rem = t - s_level[lo];
-    const int b = __builtin_amdgcn_readfirstlane(s_order[rem / heads_per_seq]);
-    const int hslot = __builtin_amdgcn_readfirstlane(rem % heads_per_seq);
-    const int part = __builtin_amdgcn_readfirstlane(lo);
-    bool claimed = false;  // by thread 0
+    s_next[slot][0] = t;
+    s_next[slot][1] = b;
+    s_next[slot][2] = hslot;
+    s_next[slot][3] = part;
+  };
+  auto ticket = [&]() -> uint32_t {
+    return __hip_atomic_fetch_add(p.queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+
+  if (tid == 0) publish(0, blockIdx.x);
+  __syncthreads();
+  // The item of iteration i is in s_next[i % 2]; thread 0 publishes the next one into the other slot
+  // during iteration i (possibly before another wave has read this iteration's slot: an item that
+  // ends early returns without a barrier), and the barrier ending iteration i makes it visible.
+  for (int slot = 0;; slot ^= 1) {
+    const int t = __builtin_amdgcn_readfirstlane(s_next[slot][0]);
+    if (t >= items) break;
+    const int b = __builtin_amdgcn_readfirstlane(s_next[slot][1]);
+    const int hslot = __builtin_amdgcn_readfirstlane(s_next[slot][2]);
+    const int part = __builtin_amdgcn_readfirstlane(s_next[slot][3]);
+    // Thread 0 only: the next ticket, claimed at the start of the item's epilogue so that the
+    // atomic's round trip overlaps the epilogue; its result is first used by publish() below.
+    uint32_t claimed = 0;
+    bool has_claim = false;
     // The thread index passes through an empty asm statement each item, so nothing computed from it
     // is hoisted out of this loop: per-lane offsets are rebuilt per item instead of holding registers
     // through every item's epilogue (hoisted, they took the 128-dim GQA-4 form to one wave per SIMD).
@@ -1172,14 +1219,18 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
     __asm__ volatile("" : "+v"(item_tid));
     partition_item<E, D, GC, true, UB, AP>(p, item_tid, b, hslot, part, [&]() __attribute__((always_inline)) {
       if (tid == 0) {
-        claim();
-        claimed = true;
+        claimed = ticket();
+        has_claim = true;
       }
     });
-    __syncthreads();
-    if (tid == 0 && !claimed) claim();
-    __syncthreads();
-    t = s_ticket;
+    if (tid == 0) {
+      if (!has_claim) claimed = ticket();
+      publish(slot ^ 1, static_cast<int>(gridDim.x + claimed));
+    }
+    // Every wave is done with the item's LDS and s_next[slot ^ 1] holds the next item.  An LDS-only
+    // barrier: the item's record stores need not be acknowledged before the next item starts (it
+    // writes other records).
+    lds_barrier();
   }
 }
 
@@ -1271,6 +1322,12 @@ bool queue_eligible(const Shape& s, int variant) {
          s.batch <= kQueueMaxBatch;
 }
 
+int queue_unsupported() {
+  return fail(RK_ERR_UNSUPPORTED,
+              "the work-queue schedule needs the MFMA variant, more than one partition per sequence "
+              "(at most %d) and at most %d sequences", kQueueMaxLevels, kQueueMaxBatch);
+}
+
 // Arrival counters of the fused launch: one 32-bit word per (sequence, KV head, head chunk).
 int64_t counter_words_for(int64_t batch, int64_t query_heads, int64_t kv_heads) {
   const int64_t group = query_heads / kv_heads;
@@ -1313,17 +1370,23 @@ hipError_t queue_capacity(int64_t* capacity) {
   return hipSuccess;
 }
 
-// The partition launch for `items` work items.  With a queue counter (prm.queue: a split-K shape
-// whose item map fits the queue kernel) the work-queue schedule runs when asked for, or, by default,
-// when the items exceed what the device holds at once; otherwise one workgroup per item.
+// The partition launch for `items` work items.  For a queue-eligible call (a split-K shape whose
+// item map fits the queue kernel; prm.queue is then its ticket counter) the work-queue schedule runs
+// when asked for, or, by default, when the items exceed what the device holds at once; otherwise one
+// workgroup per item.  With `chosen`, nothing is launched: the schedule is stored there instead.
 template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP>
-hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedule, hipStream_t stream) {
+hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedule, bool queue_ok, hipStream_t stream,
+                                   int* chosen) {
   if constexpr (QK_MFMA) {
-    if (prm.queue != nullptr) {
+    if (queue_ok) {
       int64_t capacity = 0;
       const hipError_t err = queue_capacity<E, D, GC, UB, AP>(&capacity);
       if (err != hipSuccess) return err;
       if (schedule == kScheduleQueue || items > capacity) {
+        if (chosen != nullptr) {
+          *chosen = RK_PA_SCHEDULE_QUEUE;
+          return hipSuccess;
+        }
         hipLaunchKernelGGL(pa_queue_reset_kernel, dim3(1), dim3(kWave), 0, stream, prm.queue);
         const int64_t grid = items < capacity ? items : capacity;
         hipLaunchKernelGGL((pa_partition_queue_kernel<E, D, GC, UB, AP>), dim3(static_cast<uint32_t>(grid)),
@@ -1332,38 +1395,52 @@ hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedul
       }
     }
   }
+  if (chosen != nullptr) {
+    *chosen = RK_PA_SCHEDULE_GRID;
+    return hipSuccess;
+  }
   hipLaunchKernelGGL((pa_partition_kernel<E, D, GC, QK_MFMA, UB, AP>), dim3(static_cast<uint32_t>(items)),
                      dim3(kThreads), 0, stream, prm);
   return hipGetLastError();
 }
 
+// How one call launches: its work items, schedule request, queue eligibility and stream; with
+// `chosen`, only the partition kernel's schedule is decided (and stored there), nothing launched.
+struct Launch {
+  int64_t items;
+  int schedule;
+  bool queue_ok;
+  hipStream_t stream;
+  int* chosen;
+};
+
 template <class E, int D, int GC, bool QK_MFMA, bool AP>
-hipError_t launch_partition_ub(const Params& prm, int64_t items, int schedule, hipStream_t stream) {
-  if (prm.bs_log2 >= 4) return launch_partition_kernel<E, D, GC, QK_MFMA, true, AP>(prm, items, schedule, stream);
-  return launch_partition_kernel<E, D, GC, QK_MFMA, false, AP>(prm, items, schedule, stream);
+hipError_t launch_partition_ub(const Params& prm, const Launch& l) {
+  if (prm.bs_log2 >= 4)
+    return launch_partition_kernel<E, D, GC, QK_MFMA, true, AP>(prm, l.items, l.schedule, l.queue_ok, l.stream, l.chosen);
+  return launch_partition_kernel<E, D, GC, QK_MFMA, false, AP>(prm, l.items, l.schedule, l.queue_ok, l.stream, l.chosen);
 }
 
 template <class E, int D, int GC>
-hipError_t launch_partition(const Params& prm, int variant, int64_t items, int schedule, hipStream_t stream) {
-  if (prm.new_k != nullptr)
-    return launch_partition_ub<E, D, GC, true, true>(prm, items, schedule, stream);  // validated: MFMA
-  if (variant == RK_PA_VARIANT_MFMA) return launch_partition_ub<E, D, GC, true, false>(prm, items, schedule, stream);
-  return launch_partition_ub<E, D, GC, false, false>(prm, items, schedule, stream);
+hipError_t launch_partition(const Params& prm, int variant, const Launch& l) {
+  if (prm.new_k != nullptr) return launch_partition_ub<E, D, GC, true, true>(prm, l);  // validated: MFMA
+  if (variant == RK_PA_VARIANT_MFMA) return launch_partition_ub<E, D, GC, true, false>(prm, l);
+  return launch_partition_ub<E, D, GC, false, false>(prm, l);
 }
 
 template <class E, int D>
-hipError_t launch_all(const Params& prm, int gc, int variant, int64_t grid, int schedule, bool partitions,
-                      bool reduce, hipStream_t stream) {
+hipError_t launch_all(const Params& prm, int gc, int variant, const Launch& l, bool partitions, bool reduce) {
   hipError_t err = hipSuccess;
   if (partitions) {
     if (gc == 1)
-      err = launch_partition<E, D, 1>(prm, variant, grid, schedule, stream);
+      err = launch_partition<E, D, 1>(prm, variant, l);
     else if (gc == 2)
-      err = launch_partition<E, D, 2>(prm, variant, grid, schedule, stream);
+      err = launch_partition<E, D, 2>(prm, variant, l);
     else
-      err = launch_partition<E, D, 4>(prm, variant, grid, schedule, stream);
+      err = launch_partition<E, D, 4>(prm, variant, l);
   }
-  if (err != hipSuccess || !reduce) return err;
+  if (err != hipSuccess || !reduce || l.chosen != nullptr) return err;
+  const hipStream_t stream = l.stream;
   const int64_t rows = static_cast<int64_t>(prm.batch) * prm.query_heads;
   const int64_t rgrid = (rows + kWaves - 1) / kWaves;
   hipLaunchKernelGGL((pa_reduce_kernel<E, D>), dim3(static_cast<uint32_t>(rgrid)), dim3(kThreads),
@@ -1372,11 +1449,11 @@ hipError_t launch_all(const Params& prm, int gc, int variant, int64_t grid, int 
 }
 
 template <class E>
-hipError_t launch_dtype(const Params& prm, int64_t head_dim, int gc, int variant, int64_t grid, int schedule,
-                        bool partitions, bool reduce, hipStream_t stream) {
-  if (head_dim == 64) return launch_all<E, 64>(prm, gc, variant, grid, schedule, partitions, reduce, stream);
-  if (head_dim == 128) return launch_all<E, 128>(prm, gc, variant, grid, schedule, partitions, reduce, stream);
-  return launch_all<E, 256>(prm, gc, variant, grid, schedule, partitions, reduce, stream);
+hipError_t launch_dtype(const Params& prm, int64_t head_dim, int gc, int variant, const Launch& l, bool partitions,
+                        bool reduce) {
+  if (head_dim == 64) return launch_all<E, 64>(prm, gc, variant, l, partitions, reduce);
+  if (head_dim == 128) return launch_all<E, 128>(prm, gc, variant, l, partitions, reduce);
+  return launch_all<E, 256>(prm, gc, variant, l, partitions, reduce);
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
@@ -1458,6 +1535,20 @@ constexpr int kPhaseFused = 4;  // partition kernel merging in its last workgrou
 constexpr int kPhaseAppend = 8; // partition kernel also writes each sequence's new token (AP)
 constexpr int kPhaseScratch = 16; // records in this device's `scratch` array, not `workspace`
 
+// The variant argument's kernel variant (low byte) and RK_PA_SCHEDULE_* request.
+int split_variant(int* variant, int* schedule) {
+  const int bits = *variant;
+  if ((bits & ~(RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE | 0xFF)) != 0 ||
+      (bits & (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE)) == (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE) ||
+      ((bits & 0xFF) != RK_PA_VARIANT_MFMA && (bits & 0xFF) != RK_PA_VARIANT_VALU))
+    return fail(RK_ERR_INVALID_ARGUMENT, "unknown kernel variant %d", bits);
+  *schedule = (bits & RK_PA_SCHEDULE_QUEUE) != 0 ? kScheduleQueue
+              : (bits & RK_PA_SCHEDULE_GRID) != 0 ? kScheduleGrid
+                                                  : kScheduleAuto;
+  *variant = bits & 0xFF;
+  return RK_OK;
+}
+
 int decode_phases(const void* query, const void* key_cache, const void* value_cache,
                   const void* block_tables, const void* context_lengths, void* output, void* workspace,
                   size_t workspace_bytes, int64_t batch, int64_t query_heads, int64_t kv_heads,
@@ -1479,15 +1570,8 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
     return fail(RK_ERR_INVALID_ARGUMENT, "dtype must be RK_DTYPE_FP16 or RK_DTYPE_BF16");
   if (index_dtype != RK_INDEX_INT32 && index_dtype != RK_INDEX_INT64)
     return fail(RK_ERR_INVALID_ARGUMENT, "index_dtype must be RK_INDEX_INT32 or RK_INDEX_INT64");
-  if ((variant & ~(RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE | 0xFF)) != 0 ||
-      (variant & (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE)) == (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE))
-    return fail(RK_ERR_INVALID_ARGUMENT, "unknown kernel variant %d", variant);
-  const int schedule = (variant & RK_PA_SCHEDULE_QUEUE) != 0   ? kScheduleQueue
-                       : (variant & RK_PA_SCHEDULE_GRID) != 0 ? kScheduleGrid
-                                                               : kScheduleAuto;
-  variant &= 0xFF;
-  if (variant != RK_PA_VARIANT_MFMA && variant != RK_PA_VARIANT_VALU)
-    return fail(RK_ERR_INVALID_ARGUMENT, "unknown kernel variant %d", variant);
+  int schedule = kScheduleAuto;
+  if (split_variant(&variant, &schedule) != RK_OK) return RK_ERR_INVALID_ARGUMENT;
   if (!(scale > 0.0f) || !isfinite(scale))
     return fail(RK_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
   if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(output))
@@ -1549,10 +1633,7 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   }
   const bool partitions = (phases & (kPhasePartitions | kPhaseFused)) != 0;
   const bool queue = partitions && schedule != kScheduleGrid && queue_eligible(s, variant);
-  if (partitions && schedule == kScheduleQueue && !queue)
-    return fail(RK_ERR_UNSUPPORTED,
-                "the work-queue schedule needs the MFMA variant, more than one partition per sequence "
-                "(at most %d) and at most %d sequences", kQueueMaxLevels, kQueueMaxBatch);
+  if (partitions && schedule == kScheduleQueue && !queue) return queue_unsupported();
   if (queue) prm.queue = static_cast<uint32_t*>(workspace);
   prm.counters = fused ? counters : nullptr;
   if (append) {
@@ -1577,11 +1658,9 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.scale_log2e = scale * kLog2e;
 
   const bool reduce = !fused && (phases & kPhaseReduce) != 0 && s.num_partitions > 1;
-  hipStream_t hs = static_cast<hipStream_t>(stream);
-  const hipError_t err =
-      dtype == RK_DTYPE_BF16
-          ? launch_dtype<Bf16>(prm, head_dim, gc, variant, grid, schedule, partitions, reduce, hs)
-          : launch_dtype<Fp16>(prm, head_dim, gc, variant, grid, schedule, partitions, reduce, hs);
+  const Launch l{grid, schedule, queue, static_cast<hipStream_t>(stream), nullptr};
+  const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(prm, head_dim, gc, variant, l, partitions, reduce)
+                                                : launch_dtype<Fp16>(prm, head_dim, gc, variant, l, partitions, reduce);
   if (err != hipSuccess)
     return fail(RK_ERR_LAUNCH, "paged attention launch failed: %s", hipGetErrorString(err));
   return RK_OK;
@@ -1672,6 +1751,34 @@ extern "C" int rk_pa_decode_noalloc(const void* query, const void* key_cache, co
                        batch, query_heads, kv_heads, head_dim, num_blocks, block_size,
                        max_blocks_per_sequence, scale, dtype, index_dtype, partition_tokens, variant,
                        stream, kPhasePartitions | kPhaseReduce | kPhaseScratch);
+}
+
+extern "C" int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                                     int64_t block_size, int64_t max_blocks_per_sequence, int dtype,
+                                     int64_t partition_tokens, int variant, int* schedule) {
+  if (schedule == nullptr) return fail(RK_ERR_INVALID_ARGUMENT, "schedule must not be NULL");
+  if (dtype != RK_DTYPE_FP16 && dtype != RK_DTYPE_BF16)
+    return fail(RK_ERR_INVALID_ARGUMENT, "dtype must be RK_DTYPE_FP16 or RK_DTYPE_BF16");
+  int requested = kScheduleAuto;
+  if (split_variant(&variant, &requested) != RK_OK) return RK_ERR_INVALID_ARGUMENT;
+  Shape s{batch, query_heads, kv_heads, head_dim, 1, block_size, max_blocks_per_sequence, partition_tokens, 0};
+  const int status = check_shape(s);
+  if (status != RK_OK) return status;
+  s.num_partitions = partitions_for(s);
+  const bool queue = requested != kScheduleGrid && queue_eligible(s, variant);
+  if (requested == kScheduleQueue && !queue) return queue_unsupported();
+  const int64_t group = query_heads / kv_heads;
+  const int gc = head_chunk_for(group);
+  const int64_t items = batch * kv_heads * ((group + gc - 1) / gc) * s.num_partitions;
+  Params prm{};
+  prm.bs_log2 = log2_exact(block_size);
+  int chosen = RK_PA_SCHEDULE_GRID;
+  const Launch l{items, requested, queue, nullptr, &chosen};
+  const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(prm, head_dim, gc, variant, l, true, false)
+                                                : launch_dtype<Fp16>(prm, head_dim, gc, variant, l, true, false);
+  if (err != hipSuccess) return fail(RK_ERR_LAUNCH, "schedule query failed: %s", hipGetErrorString(err));
+  *schedule = chosen;
+  return RK_OK;
 }
 
 extern "C" const char* rk_pa_last_error(void) { return g_last_error.c_str(); }

@@ -12,9 +12,9 @@
 //   "fused"   the single-launch form (rk_pa_decode_fused): the partition kernel's last workgroup per
 //             (sequence, head slot) merges; it saves the reduce launch but every workgroup then
 //             waits for its records' write-through and one counter round trip before it exits;
-//   "auto"    fused for grids under kFusedMergeMaxItems workgroups (one or a few rounds on the
-//             256 CUs, where the saved launch dominates: 8-9% faster on 256-workgroup grids),
-//             reduce above (0.5% faster at 8192 workgroups, where the per-workgroup wait adds up).
+//   "auto"    fused: 8-9% faster on 256-workgroup grids, where the saved launch dominates, and 1%
+//             faster on the 128-sequence ragged workload's 8192 work items, which run on the
+//             work-queue schedule (the grid schedule there was 0.5% slower fused than reduce).
 // The fused form's arrival counters live in one zero-initialised buffer per (device, stream),
 // created on first use and kept for the life of the process; every completed call leaves it zero
 // for the next call on that stream.  Calls made while the stream is being captured into a graph
@@ -87,14 +87,12 @@ bool capturing(hipStream_t stream) {
   return status != hipStreamCaptureStatusNone;
 }
 
-constexpr int64_t kFusedMergeMaxItems = 4096;
-
-bool fused_merge_requested(const std::string& merge, int64_t items) {
+bool fused_merge_requested(const std::string& merge) {
   if (merge == "fused") return true;
   if (merge == "reduce") return false;
   TORCH_CHECK_VALUE(merge == "auto", "rk_pa_gfx950: merge must be \"auto\", \"fused\" or \"reduce\" (got \"",
                     merge, "\")");
-  return items < kFusedMergeMaxItems;
+  return true;
 }
 
 // new_key / new_value: undefined for a plain decode; for append-and-decode the [batch, kv_heads,
@@ -169,8 +167,7 @@ at::Tensor decode(const at::Tensor& query, const at::Tensor& key_cache,
   size_t words = 0;
   status = rk_pa_decode_counter_words(batch, query_heads, kv_heads, &words);
   if (status != RK_OK) raise_status(status);
-  const int64_t partitions = (max_blocks * block_size + partition_tokens - 1) / partition_tokens;
-  const bool fused = fused_merge_requested(merge, static_cast<int64_t>(words) * partitions);
+  const bool fused = fused_merge_requested(merge);
   if (append) {
     uint32_t* counters = fused && workspace_bytes > 0 && !capturing(stream) ? stream_counters(query, stream, words)
                                                                             : nullptr;

@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "rk_pa_decode_counter_words",
     "rk_pa_decode_workspace_bytes",
     "rk_pa_decode_noalloc",
+    "rk_pa_decode_schedule",
     "rk_pa_last_error",
     "rk_pa_version",
 )
@@ -95,6 +96,9 @@ class PagedAttentionLibrary:
         lib.rk_pa_decode_noalloc.restype = ctypes.c_int
         lib.rk_pa_decode_counter_words.argtypes = [i64, i64, i64, ctypes.POINTER(sz)]
         lib.rk_pa_decode_counter_words.restype = ctypes.c_int
+        lib.rk_pa_decode_schedule.argtypes = [i64, i64, i64, i64, i64, i64, ctypes.c_int, i64, ctypes.c_int,
+                                              ctypes.POINTER(ctypes.c_int)]
+        lib.rk_pa_decode_schedule.restype = ctypes.c_int
         lib.rk_pa_last_error.argtypes = []
         lib.rk_pa_last_error.restype = ctypes.c_char_p
         lib.rk_pa_version.argtypes = []
@@ -110,6 +114,19 @@ class PagedAttentionLibrary:
     def check(self, status: int) -> None:
         if status != RK_OK:
             raise CabiError(status, self.last_error())
+
+    def schedule(self, batch: int, query_heads: int, kv_heads: int, head_dim: int, block_size: int,
+                 max_blocks: int, dtype: str, partition_tokens: int, variant: str = "mfma",
+                 schedule: str = "auto") -> str:
+        """``"grid"`` or ``"queue"``: the partition-kernel schedule a decode with these arguments runs on
+        the current device (rk_pa_decode_schedule)."""
+
+        out = ctypes.c_int(0)
+        self.check(self.lib.rk_pa_decode_schedule(batch, query_heads, kv_heads, head_dim, block_size, max_blocks,
+                                                  RK_DTYPE_BF16 if dtype == "bf16" else RK_DTYPE_FP16,
+                                                  partition_tokens, VARIANTS[variant] | SCHEDULES[schedule],
+                                                  ctypes.byref(out)))
+        return {SCHEDULES["grid"]: "grid", SCHEDULES["queue"]: "queue"}[out.value]
 
     def workspace_bytes(self, batch: int, query_heads: int, head_dim: int, block_size: int, max_blocks: int,
                         partition_tokens: int) -> int:

@@ -11,10 +11,9 @@ Operators and regions:
   in each dtype, plus the 128-sequence ragged shape, with the partition size chosen for that shape
   (``launch.partition_tokens``) and how its partition records
   are merged (``launch.merge``: ``fused`` -- the partition kernel's last workgroup per sequence and
-  head slot merges, one launch -- measured 7-12% faster on the 256-workgroup shapes; ``reduce`` -- a
-  separate reduce launch, 0.5% faster on the 8192-workgroup ragged batch), and one broad gfx950
-  region (priority 10) covering every shape the library accepts with ``merge: auto`` (fused below
-  4096 workgroups);
+  head slot merges, one launch -- measured 7-12% faster on the 256-workgroup shapes and 1-2% faster
+  on the ragged batch's work queue; ``reduce`` -- a separate reduce launch), and one broad gfx950
+  region (priority 10) covering every shape the library accepts with ``merge: auto`` (fused);
 * ``kv_cache_append`` and ``kv_cache_copy``: one exact entry per case of the reference's workload files
   (benchmarks/workloads/kv_cache_append-1.0.yaml:12-18, kv_cache_copy-1.0.yaml:12-17) and one broad
   gfx950 region each; their bindings (entrypoints ``append`` and ``copy``) share one kernel source;
@@ -105,7 +104,10 @@ EXACT_REGIONS: list[tuple[str, dict[str, Any], dict[str, Any]]] = [
         "b128-gqa32x8-ragged-d128-p16-bf16",
         {"dtype": "bf16", "batch": 128, "query_heads": 32, "kv_heads": 8, "head_dim": 128,
          "num_blocks": [1, _INT_MAX], "block_size": 16, "max_blocks_per_sequence": 1024},
-        {"partition_tokens": 2048, "merge": "reduce"},
+        # Work-queue schedule (the library's choice for its 8192 work items): partitions of 4096
+        # tokens, the table's limit at 16-token blocks, measured fastest (646.8 us per call against
+        # 656.6 at 2048 and 651.9 at 3072, fused).
+        {"partition_tokens": 4096, "merge": "fused"},
     ),
 ]
 

@@ -156,6 +156,31 @@ def test_invalid_arguments_are_rejected_before_launch(lib, overrides, status, me
     assert message in text
 
 
+@pytest.mark.parametrize(
+    "overrides, status, message",
+    [
+        (dict(dtype=5), cabi.RK_ERR_INVALID_ARGUMENT, "dtype"),
+        (dict(variant=0x300), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        (dict(variant=7), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        (dict(head_dim=96), cabi.RK_ERR_INVALID_ARGUMENT, "one of 64, 128, 256"),
+        (dict(variant=0x200, max_blocks=4), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
+        (dict(variant=0x201), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
+    ],
+)
+def test_schedule_query_validates_before_asking_the_device(lib, overrides, status, message):
+    """rk_pa_decode_schedule rejects what a decode would reject, before any runtime query."""
+
+    args = dict(batch=8, query_heads=32, kv_heads=8, head_dim=128, block_size=16, max_blocks=64, dtype=1,
+                partition_tokens=256, variant=0)
+    args.update(overrides)
+    out = ctypes.c_int(-1)
+    got = lib.lib.rk_pa_decode_schedule(*args.values(), ctypes.byref(out))
+    assert got == status, lib.last_error()
+    assert message in lib.last_error()
+    assert out.value == -1
+    assert lib.lib.rk_pa_decode_schedule(8, 32, 8, 128, 16, 64, 1, 256, 0, None) == cabi.RK_ERR_INVALID_ARGUMENT
+
+
 @cpu_only
 def test_phase_entry_points_validate_identically(lib):
     for phase in ("partitions", "reduce"):

@@ -192,3 +192,21 @@ def test_ragged_b128_workload_schedules_agree(gpu, palib, c5_case):
     auto = palib.decode(*args, partition_tokens=2048)
     torch.cuda.synchronize()
     assert same_bits(auto, grid)
+
+
+def test_schedule_query_names_what_runs(gpu, palib):
+    """rk_pa_decode_schedule: the ragged 128-sequence workload (8192 items) takes the queue, a grid
+    the device holds at once keeps one workgroup per item, and the forcing bits are reported back."""
+
+    from benchmarks.workloads import WORKLOADS
+
+    announce("schedule query")
+    for key, partition, expected in (("c5", 4096, "queue"), ("c5", 2048, "queue"), ("c2", 256, "grid"),
+                                     ("c3", 512, "grid"), ("c1", 128, "grid")):
+        w = WORKLOADS[key]
+        args = (w.batch, w.query_heads, w.kv_heads, w.head_dim, w.block_size, w.max_blocks, w.dtype, partition)
+        assert palib.schedule(*args) == expected, key
+        assert palib.schedule(*args, schedule="grid") == "grid"
+        if partition < w.max_blocks * w.block_size:  # split-K: the queue can be forced
+            assert palib.schedule(*args, schedule="queue") == "queue"
+    assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 2048, variant="valu") == "grid"

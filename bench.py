@@ -52,7 +52,9 @@ for entry in (str(ROOT / "radeon-kernels_amd"), str(ROOT)):
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "paged-attn decode µs/call + effective KV GB/s (% MI355X HBM peak), b128"
-TRAFFIC_SUMMARY = ROOT / "profiles" / "pa_partition_kernel_b128_traffic.txt"
+# Committed counter summaries of the partition kernel on the 128-sequence workload, one per schedule.
+TRAFFIC_SUMMARIES = (ROOT / "profiles" / "pa_partition_queue_kernel_b128_traffic.txt",
+                     ROOT / "profiles" / "pa_partition_kernel_b128_traffic.txt")
 
 
 def parse_args(argv=None):
@@ -152,26 +154,27 @@ def dispatch_launch(torch, q, k, v, bt, cl) -> dict:
     return rk.get_last_dispatch()
 
 
-def read_traffic(workload: str, variant: str, partition: int, merge: str, kv_bytes: int):
-    """HBM bytes per partition-kernel launch from the committed counter summary, if it was measured
-    on exactly this configuration: workload, variant, partition size, merge form and the same input
-    draw (its KV bytes per call)."""
+def read_traffic(workload: str, variant: str, partition: int, merge: str, schedule: str, kv_bytes: int):
+    """HBM bytes per partition-kernel launch from a committed counter summary, if one was measured
+    on exactly this configuration: workload, variant, partition size, merge form, schedule and the
+    same input draw (its KV bytes per call)."""
 
-    if not TRAFFIC_SUMMARY.is_file():
-        return None
-    fields = {}
-    for line in TRAFFIC_SUMMARY.read_text().splitlines():
-        if "=" in line and not line.lstrip().startswith("#"):
-            key, value = line.split("=", 1)
-            fields[key.strip()] = value.strip()
-    try:
-        if (fields.get("workload") != workload or fields.get("variant") != variant
-                or int(fields["partition_tokens"]) != partition or fields.get("merge", "reduce") != merge
-                or int(fields["kv_bytes_per_call"]) != kv_bytes):
-            return None
-        return int(fields["hbm_bytes_per_launch"])
-    except (KeyError, ValueError):
-        return None
+    for summary in TRAFFIC_SUMMARIES:
+        if not summary.is_file():
+            continue
+        fields = {}
+        for line in summary.read_text().splitlines():
+            if "=" in line and not line.lstrip().startswith("#"):
+                key, value = line.split("=", 1)
+                fields[key.strip()] = value.strip()
+        try:
+            if (fields.get("workload") == workload and fields.get("variant") == variant
+                    and int(fields["partition_tokens"]) == partition and fields.get("merge", "reduce") == merge
+                    and fields.get("schedule", "grid") == schedule and int(fields["kv_bytes_per_call"]) == kv_bytes):
+                return int(fields["hbm_bytes_per_launch"])
+        except (KeyError, ValueError):
+            continue
+    return None
 
 
 PHASE_SYMBOL = {"all": "rk_pa_decode", "fused": "rk_pa_decode_fused"}
@@ -728,7 +731,7 @@ def main(argv=None) -> int:
                 "us_per_step_one_launch": round(one, 2), "entrypoints": ["rk_kv_cache_append + " + PHASE_SYMBOL[headline],
                                                                          "rk_pa_decode_append"]}
 
-    traffic = read_traffic(w.name, variant, partition, merge, kv_bytes)
+    traffic = read_traffic(w.name, variant, partition, merge, schedule, kv_bytes)
     result = {
         "metric": METRIC,
         "value": round(gbps, 1),

@@ -83,18 +83,20 @@ def test_bench_reads_traffic_only_for_its_exact_configuration(tmp_path, monkeypa
     summary = tmp_path / "traffic.txt"
     summary.write_text("# measured\nworkload = b128-x\nvariant = mfma\npartition_tokens = 2048\n"
                        "kv_bytes_per_call = 4237918208\nhbm_bytes_per_launch = 4867000000\n")
-    monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", summary)
+    monkeypatch.setattr(bench, "TRAFFIC_SUMMARIES", (tmp_path / "absent.txt", summary))
     kv = 4_237_918_208
-    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv) == 4_867_000_000
-    assert bench.read_traffic("b128-x", "mfma", 1024, "reduce", kv) is None
-    assert bench.read_traffic("other", "mfma", 2048, "reduce", kv) is None
-    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv + 1) is None  # another input draw
-    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", kv) is None  # measured in the reduce form
-    summary.write_text(summary.read_text() + "merge = fused\n")
-    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", kv) == 4_867_000_000
-    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv) is None
-    monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", tmp_path / "absent.txt")
-    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", kv) is None
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", "grid", kv) == 4_867_000_000
+    assert bench.read_traffic("b128-x", "mfma", 1024, "reduce", "grid", kv) is None
+    assert bench.read_traffic("other", "mfma", 2048, "reduce", "grid", kv) is None
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", "grid", kv + 1) is None  # another input draw
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "grid", kv) is None  # measured in the reduce form
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", "queue", kv) is None  # and on the grid schedule
+    summary.write_text(summary.read_text() + "merge = fused\nschedule = queue\n")
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "queue", kv) == 4_867_000_000
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "grid", kv) is None
+    assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", "queue", kv) is None
+    monkeypatch.setattr(bench, "TRAFFIC_SUMMARIES", (tmp_path / "absent.txt",))
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "queue", kv) is None
 
 
 def test_case_traffic_matches_operator_case_and_dtype(tmp_path):

@@ -265,9 +265,6 @@ struct Params {
   // Fused merge only (else null): [batch, kv_heads * head_chunks] arrival counters, zero on entry,
   // left zero on exit (the last arriver resets its counter).
   uint32_t* __restrict__ counters;
-  // Work-queue schedule only (else null): the ticket counter, zeroed by pa_queue_reset_kernel in
-  // front of every queue launch.
-  uint32_t* __restrict__ queue;
   // Append-and-decode only (else null): [batch, kv_heads, D] K and V rows of each sequence's new
   // token (position context_length - 1).  The kernel attends to them from these buffers and stores
   // them into that position's cache slot; k_store / v_store are the caches' base addresses.
@@ -289,6 +286,10 @@ struct Params {
   int32_t num_partitions;  // ceil(max_blocks * BS / partition_tokens)
   int32_t index_is64;
   float scale_log2e;
+  // Work-queue schedule only (else null): the ticket counter, zeroed by pa_queue_reset_kernel in
+  // front of every queue launch.  Last, so the fields before it keep the grid kernel's argument
+  // layout.
+  uint32_t* __restrict__ queue;
 };
 
 __device__ __forceinline__ int64_t clamped_context(const Params& p, int b) {

@@ -81,8 +81,10 @@ extern "C" {
  *   RK_PA_SCHEDULE_GRID   one workgroup per work item, items past a sequence's context included
  *                         (they exit at once).
  *   RK_PA_SCHEDULE_QUEUE  as many workgroups as the device holds at once take the items that
- *                         hold tokens from a ticket counter in the workspace header (a one-thread
- *                         kernel zeroes it first).  Eligible: RK_PA_VARIANT_MFMA, a split-K shape
+ *                         hold tokens from a ticket counter: in the workspace header, zeroed by a
+ *                         one-thread kernel launched first, or, for rk_pa_decode_fused and the fused
+ *                         rk_pa_decode_append, in the last two words of the counter array, which the
+ *                         launch's last workgroup leaves zero (one launch).  Eligible: RK_PA_VARIANT_MFMA, a split-K shape
  *                         (rk_pa_decode_workspace_bytes > 0) with at most 256 partitions per
  *                         sequence and at most 1024 sequences; RK_ERR_UNSUPPORTED otherwise.
  */
@@ -160,8 +162,9 @@ int rk_pa_decode_reduce(const void* query, const void* key_cache, const void* va
  * partition of that sequence in partition order; no reduce launch follows.  Results agree with
  * rk_pa_decode to fp32 rounding of the final merge (both are deterministic).
  *
- * counters/counter_words: device array of at least rk_pa_decode_counter_words(...) uint32 words.
- *   It must be all zero before the first call (e.g. hipMemset once at allocation); every call
+ * counters/counter_words: device array of at least rk_pa_decode_counter_words(...) uint32 words: one
+ *   arrival counter per (sequence, KV head, head chunk), then the work-queue schedule's ticket and exit
+ *   counters.  It must be all zero before the first call (e.g. hipMemset once at allocation); every call
  *   that completes leaves it all zero again, so one buffer serves any number of calls in stream
  *   order.  Calls that may run concurrently (different streams) need separate counter buffers
  *   and separate workspaces.  Ignored (may be NULL) when rk_pa_decode_workspace_bytes is zero.

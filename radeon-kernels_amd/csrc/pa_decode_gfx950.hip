@@ -286,10 +286,13 @@ struct Params {
   int32_t num_partitions;  // ceil(max_blocks * BS / partition_tokens)
   int32_t index_is64;
   float scale_log2e;
-  // Work-queue schedule only (else null): the ticket counter, zeroed by pa_queue_reset_kernel in
-  // front of every queue launch.  Last, so the fields before it keep the grid kernel's argument
-  // layout.
+  // Work-queue schedule only (else null), last so the fields before them keep the grid kernel's
+  // argument layout.  queue: the ticket counter.  queue_done: null when the counter sits in the
+  // workspace header and pa_queue_reset_kernel zeroes it in front of every launch; otherwise (fused
+  // launch: both words at the end of the arrival-counter array, zero on entry) the workgroups count
+  // their exits on it and the last one zeroes both words for the next call.
   uint32_t* __restrict__ queue;
+  uint32_t* __restrict__ queue_done;
 };
 
 __device__ __forceinline__ int64_t clamped_context(const Params& p, int b) {
@@ -1233,6 +1236,15 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
     // writes other records).
     lds_barrier();
   }
+  // Self-resetting counter: every ticket this workgroup claimed has returned (its value was used), so
+  // when the last workgroup counts its exit no claim is outstanding and both words can be zeroed.
+  if (p.queue_done != nullptr && tid == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(p.queue_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1) {
+      __hip_atomic_store(p.queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.queue_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // Zeroes the work-queue ticket counter in front of a queue launch (a kernel, not a memset, so the
@@ -1329,11 +1341,16 @@ int queue_unsupported() {
               "(at most %d) and at most %d sequences", kQueueMaxLevels, kQueueMaxBatch);
 }
 
-// Arrival counters of the fused launch: one 32-bit word per (sequence, KV head, head chunk).
-int64_t counter_words_for(int64_t batch, int64_t query_heads, int64_t kv_heads) {
+// Counters of the fused launch: one 32-bit arrival counter per (sequence, KV head, head chunk), then
+// the work queue's ticket and exit counters.
+constexpr int64_t kQueueCounterWords = 2;
+int64_t arrival_words_for(int64_t batch, int64_t query_heads, int64_t kv_heads) {
   const int64_t group = query_heads / kv_heads;
   const int64_t gc = group == 1 ? 1 : (group == 2 ? 2 : 4);
   return batch * kv_heads * ((group + gc - 1) / gc);
+}
+int64_t counter_words_for(int64_t batch, int64_t query_heads, int64_t kv_heads) {
+  return arrival_words_for(batch, query_heads, kv_heads) + kQueueCounterWords;
 }
 
 // Schedule requests (the RK_PA_SCHEDULE_* bits of the variant argument).
@@ -1388,7 +1405,8 @@ hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedul
           *chosen = RK_PA_SCHEDULE_QUEUE;
           return hipSuccess;
         }
-        hipLaunchKernelGGL(pa_queue_reset_kernel, dim3(1), dim3(kWave), 0, stream, prm.queue);
+        if (prm.queue_done == nullptr)
+          hipLaunchKernelGGL(pa_queue_reset_kernel, dim3(1), dim3(kWave), 0, stream, prm.queue);
         const int64_t grid = items < capacity ? items : capacity;
         hipLaunchKernelGGL((pa_partition_queue_kernel<E, D, GC, UB, AP>), dim3(static_cast<uint32_t>(grid)),
                            dim3(kThreads), 0, stream, prm);
@@ -1608,7 +1626,7 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   if (fused) {
     const size_t words = static_cast<size_t>(counter_words_for(batch, query_heads, kv_heads));
     if (counters == nullptr || counter_words < words)
-      return fail(RK_ERR_WORKSPACE, "%zu arrival counters required, %zu given", words, counter_words);
+      return fail(RK_ERR_WORKSPACE, "%zu counter words required, %zu given", words, counter_words);
     if ((reinterpret_cast<uintptr_t>(counters) & 3u) != 0)
       return fail(RK_ERR_WORKSPACE, "counters must be 4-byte aligned");
   }
@@ -1635,7 +1653,12 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   const bool partitions = (phases & (kPhasePartitions | kPhaseFused)) != 0;
   const bool queue = partitions && schedule != kScheduleGrid && queue_eligible(s, variant);
   if (partitions && schedule == kScheduleQueue && !queue) return queue_unsupported();
-  if (queue) prm.queue = static_cast<uint32_t*>(workspace);
+  if (queue && fused) {  // the ticket and exit counters after the arrival counters, zero on entry
+    prm.queue = counters + arrival_words_for(batch, query_heads, kv_heads);
+    prm.queue_done = prm.queue + 1;
+  } else if (queue) {  // the workspace header, zeroed by a kernel in front of the launch
+    prm.queue = static_cast<uint32_t*>(workspace);
+  }
   prm.counters = fused ? counters : nullptr;
   if (append) {
     prm.new_k = static_cast<const uint16_t*>(new_key);

@@ -192,11 +192,12 @@ def test_phase_entry_points_validate_identically(lib):
 
 
 def test_counter_words_formula(lib):
-    """One arrival counter per (sequence, KV head, head chunk); chunks hold 1, 2 or 4 query heads."""
+    """One arrival counter per (sequence, KV head, head chunk), chunks of 1, 2 or 4 query heads, then the
+    work queue's ticket and exit counters."""
 
-    for batch, hq, hkv, expected in [(128, 32, 8, 128 * 8), (3, 64, 8, 3 * 8 * 2), (2, 12, 4, 2 * 4),
+    for batch, hq, hkv, arrivals in [(128, 32, 8, 128 * 8), (3, 64, 8, 3 * 8 * 2), (2, 12, 4, 2 * 4),
                                      (5, 8, 8, 40), (1, 16, 8, 8), (2, 40, 8, 2 * 8 * 2)]:
-        assert lib.counter_words(batch, hq, hkv) == expected
+        assert lib.counter_words(batch, hq, hkv) == arrivals + 2
     out = ctypes.c_size_t(0)
     assert lib.lib.rk_pa_decode_counter_words(1, 8, 2, None) == cabi.RK_ERR_INVALID_ARGUMENT
     assert lib.lib.rk_pa_decode_counter_words(1, 9, 2, ctypes.byref(out)) == cabi.RK_ERR_INVALID_ARGUMENT
@@ -207,15 +208,16 @@ def test_counter_words_formula(lib):
 @pytest.mark.parametrize(
     "overrides, status, message",
     [
-        (dict(counters=0, counter_words=0), cabi.RK_ERR_WORKSPACE, "arrival counters required"),
-        (dict(counters=4096, counter_words=3), cabi.RK_ERR_WORKSPACE, "4 arrival counters required, 3 given"),
+        (dict(counters=0, counter_words=0), cabi.RK_ERR_WORKSPACE, "counter words required"),
+        (dict(counters=4096, counter_words=5), cabi.RK_ERR_WORKSPACE, "6 counter words required, 5 given"),
         (dict(counters=4098, counter_words=64), cabi.RK_ERR_WORKSPACE, "4-byte aligned"),
         (dict(query=0), cabi.RK_ERR_INVALID_ARGUMENT, "must not be NULL"),
         (dict(workspace=0, workspace_bytes=0), cabi.RK_ERR_WORKSPACE, "workspace of"),
     ],
 )
 def test_fused_entry_validates_counters_before_launch(lib, overrides, status, message):
-    # batch 2, 8 query heads over 2 KV heads (one chunk of 4) -> 4 counters; 4 partitions of 64 tokens.
+    # batch 2, 8 query heads over 2 KV heads (one chunk of 4) -> 4 arrival counters and the queue's 2; 4
+    # partitions of 64 tokens.
     args = dict(phase="fused", max_blocks=16, workspace=1 << 20, workspace_bytes=1 << 20, counters=4096,
                 counter_words=64)
     args.update(overrides)

@@ -74,9 +74,9 @@ extern "C" {
 
 /*
  * Schedule of the partition kernel, OR-ed into the variant argument (no reference counterpart).
- * Without either bit the library chooses: the work queue when the call is eligible for it and its
+ * Without either bit the library chooses: the work queue when the call is eligible for it, its
  * work items (sequence x KV head x head chunk x partition) exceed the workgroups the device holds
- * at once, else one workgroup per work item.  Both schedules compute every item the same way, so
+ * at once and partition_tokens >= 256, else one workgroup per work item.  Both schedules compute every item the same way, so
  * outputs are bit-identical.
  *   RK_PA_SCHEDULE_GRID   one workgroup per work item, items past a sequence's context included
  *                         (they exit at once).

@@ -53,6 +53,12 @@ constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, p
 // Work-queue schedule limits: sequences and partition levels whose item map fits in LDS.
 constexpr int kQueueMaxBatch = 1024;
 constexpr int kQueueMaxLevels = 256;
+// Smallest partition the automatic choice runs on the queue.  Below it items are a tile or two per
+// wave and the queue's per-item claim and barriers cost more than the grid's launches: 1024
+// sequences of 64-512 tokens at P 64 measured 654 against 629 us, of 64-1024 tokens at P 128 709
+// against 701 us; at P 256 every shape measured tied or won (1024 x 256-2048 tokens: 1061 against
+// 1113 us).
+constexpr int kQueueMinPartitionTokens = 256;
 constexpr size_t kQueueHeaderBytes = 256;  // workspace bytes in front of the split-K records
 constexpr float kLog2e = 1.4426950408889634f;
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory operations are
@@ -1067,6 +1073,83 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   partition_item<E, D, GC, QK_MFMA, UB, AP>(p, static_cast<int>(threadIdx.x), b, hslot, part, [] {});
 }
 
+// Item-map helpers of the work-queue kernel.  kQueueBins counts the key values of its two sorts: a
+// sequence's full-partition count (0..256) and the 64-token size class of its partial partition
+// (0..128).
+constexpr int kQueueBins = 320;
+constexpr int kQueueClassTokens = 64;
+
+// Wave 0: s_count[v] <- number of sorted sequences whose key exceeds v, for every bin v.
+__device__ __forceinline__ void descending_offsets(int* s_count, int lane) {
+  constexpr int PER = kQueueBins / kWave;
+  int v[PER];
+  int local = 0;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    v[e] = s_count[lane * PER + e];
+    local += v[e];
+  }
+  int suffix = local;  // this lane's bins and every higher lane's
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int other = __shfl_down(suffix, off);
+    if (lane + off < kWave) suffix += other;
+  }
+  int run = suffix - local;
+#pragma unroll
+  for (int e = PER - 1; e >= 0; --e) {
+    s_count[lane * PER + e] = run;
+    run += v[e];
+  }
+}
+
+// Stable counting sort, by descending key, of the sequences whose key(i) is >= 0 (keys below
+// kQueueBins) into order[]; every workgroup computes the same order.  before_rounds(s_count) runs
+// once the bins hold the descending offsets (s_count[v] = sequences with a larger key).  The
+// sequences are placed in rounds of one per thread, in index order: a sequence's position is its
+// key's offset, plus the sequences of that key placed in earlier rounds, plus those of lower thread
+// index in this round.  O(batch) work per thread for the histogram and at most 256 key compares
+// per round, against the O(batch) compares per sequence of a plain rank.
+template <class Key, class Hook>
+__device__ __attribute__((always_inline)) inline int queue_sort(int batch, int tid, Key&& key, uint16_t* order,
+                                                                int* s_count, int16_t* s_round, Hook&& before_rounds) {
+  for (int v = tid; v < kQueueBins; v += kThreads) s_count[v] = 0;
+  __syncthreads();
+  for (int i = tid; i < batch; i += kThreads) {
+    const int k = key(i);
+    if (k >= 0) atomicAdd(&s_count[k], 1);
+  }
+  __syncthreads();
+  if (tid < kWave) descending_offsets(s_count, tid);
+  __syncthreads();
+  before_rounds(s_count);
+  __syncthreads();
+  int placed = 0;
+  for (int base = 0; base < batch; base += kThreads) {
+    const int i = base + tid;
+    const int k = i < batch ? key(i) : -1;
+    s_round[tid] = static_cast<int16_t>(k);
+    __syncthreads();
+    if (k >= 0) {
+      int rank = 0;
+      for (int o = 0; o < tid; o += 8) {  // eight keys per 16-byte LDS read
+        const u32x4 w = *reinterpret_cast<const u32x4*>(s_round + o);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int other = static_cast<int16_t>(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
+          rank += (o + e < tid && other == k) ? 1 : 0;
+        }
+      }
+      order[s_count[k] + rank] = static_cast<uint16_t>(i);
+      ++placed;
+    }
+    __syncthreads();
+    if (k >= 0) atomicAdd(&s_count[k], 1);
+    __syncthreads();
+  }
+  return placed;
+}
+
 // Work-queue schedule: as many workgroups as the device holds at once, each running work items
 // until none is left.  A grid of one workgroup per item pays a workgroup launch per item (the
 // per-workgroup timeline of the 128-sequence ragged workload showed 2-12 us between one
@@ -1079,9 +1162,10 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 // not divide c, one partial partition of c % P tokens; a context <= 0 has one partial partition of
 // no tokens (its item writes the NaN row).  Items are numbered largest first: the full partitions
 // level by level (level k: partition k of every sequence with more than k full partitions, the
-// sequences by full count, largest first, ties by index), then the partial partitions by size,
-// largest first (ties by index); the head slot is fastest throughout.  The smallest items come last,
-// so the workgroups run out of work at nearly the same time.
+// sequences by full count, largest first, ties by index), then the partial partitions by size class
+// (64-token steps), largest first (ties by index); the head slot is fastest throughout.  The smallest
+// items come last, so the workgroups run out of work at nearly the same time.  Both orders are
+// stable counting sorts (queue_sort).
 //
 // Workgroup w runs item w first; every further item comes from the ticket counter
 // (gridDim.x + ticket).  Thread 0 claims its workgroup's next ticket at the start of the current
@@ -1093,10 +1177,13 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
 template <class E, int D, int GC, bool UB, bool AP>
 __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) {
   __shared__ uint16_t s_full[kQueueMaxBatch];        // full partitions of sequence b
-  __shared__ int16_t s_partial[kQueueMaxBatch];      // tokens of its partial partition, -1: none
+  __shared__ int16_t s_class[kQueueMaxBatch];        // size class of its partial partition, -1: none
   __shared__ uint16_t s_full_order[kQueueMaxBatch];  // sequences by full count, descending
-  __shared__ uint16_t s_part_order[kQueueMaxBatch];  // sequences with a partial, by its size, descending
+  __shared__ uint16_t s_part_order[kQueueMaxBatch];  // sequences with a partial, by size class, descending
   __shared__ int s_level[kQueueMaxLevels + 1];       // first item of each full level; [levels] = full items
+  __shared__ int s_count[kQueueBins];
+  __shared__ __attribute__((aligned(16))) int16_t s_round[kThreads];
+  __shared__ int s_levels;
   __shared__ int s_partials;
   __shared__ int s_next[2][4];  // ticket, sequence, head slot, partition; by item parity
   const int tid = threadIdx.x;
@@ -1106,44 +1193,28 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
   const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << p.bs_log2;
   const int P = p.partition_tokens;
 
-  if (tid == 0) s_partials = 0;
+  if (tid == 0) {
+    s_levels = 0;
+    s_partials = 0;
+  }
   for (int i = tid; i < p.batch; i += kThreads) {
     const int64_t c = index_value(load_raw_index(p.context_lengths, i, is64), is64);
     const int cc = static_cast<int>(c < max_ctx ? c : max_ctx);
+    const int rem = cc <= 0 ? 0 : cc % P;
     s_full[i] = static_cast<uint16_t>(cc <= 0 ? 0 : cc / P);
-    s_partial[i] = static_cast<int16_t>(cc <= 0 ? 0 : (cc % P != 0 ? cc % P : -1));
+    s_class[i] = static_cast<int16_t>(cc > 0 && rem == 0 ? -1 : (rem + kQueueClassTokens - 1) / kQueueClassTokens);
   }
   __syncthreads();
-  // Stable ranks: by full count, and (sequences with a partial) by partial size, both descending.
-  int partials = 0;
-  for (int i = tid; i < p.batch; i += kThreads) {
-    const int full = s_full[i], part_size = s_partial[i];
-    int full_pos = 0, part_pos = 0;
-    for (int o = 0; o < p.batch; ++o) {
-      const int other_full = s_full[o], other_part = s_partial[o];
-      full_pos += (other_full > full || (other_full == full && o < i)) ? 1 : 0;
-      part_pos += (other_part > part_size || (other_part == part_size && o < i)) ? 1 : 0;
-    }
-    s_full_order[full_pos] = static_cast<uint16_t>(i);
-    if (part_size >= 0) {
-      s_part_order[part_pos] = static_cast<uint16_t>(i);
-      ++partials;
-    }
-  }
-  if (partials > 0) atomicAdd(&s_partials, partials);
-  __syncthreads();
-  // Full level k holds the sequences whose full count exceeds k: a prefix of the order, found by
-  // bisection.
-  const int levels = s_full[s_full_order[0]];
-  for (int k = tid; k < levels; k += kThreads) {
-    int lo = 0, hi = p.batch;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (s_full[s_full_order[mid]] > k) lo = mid + 1; else hi = mid;
-    }
-    s_level[k + 1] = lo * heads_per_seq;
-  }
-  __syncthreads();
+  // Full order.  Before its rounds the bins hold, for level k, the number of sequences with more than
+  // k full partitions: the level's size.
+  queue_sort(p.batch, tid, [&](int i) { return static_cast<int>(s_full[i]); }, s_full_order, s_count, s_round,
+             [&](const int* count) {
+               for (int v = tid; v < kQueueMaxLevels; v += kThreads) {
+                 s_level[v + 1] = count[v] * heads_per_seq;
+                 if (count[v] > 0) atomicMax(&s_levels, v + 1);
+               }
+             });
+  const int levels = __builtin_amdgcn_readfirstlane(s_levels);
   if (tid < kWave) {  // exclusive prefix over the levels: four per lane, then a wave scan
     constexpr int PER = kQueueMaxLevels / kWave;
     int v[PER];
@@ -1169,6 +1240,10 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
     }
     if (lane == 0) s_level[0] = 0;
   }
+  // Partial order (its bins are free again: the full order's rounds are done).
+  const int placed = queue_sort(p.batch, tid, [&](int i) { return static_cast<int>(s_class[i]); }, s_part_order,
+                                s_count, s_round, [](const int*) {});
+  if (placed > 0) atomicAdd(&s_partials, placed);
   __syncthreads();
   const int full_items = __builtin_amdgcn_readfirstlane(s_level[levels]);
   const int items = full_items + __builtin_amdgcn_readfirstlane(s_partials) * heads_per_seq;
@@ -1390,8 +1465,8 @@ hipError_t queue_capacity(int64_t* capacity) {
 
 // The partition launch for `items` work items.  For a queue-eligible call (a split-K shape whose
 // item map fits the queue kernel; prm.queue is then its ticket counter) the work-queue schedule runs
-// when asked for, or, by default, when the items exceed what the device holds at once; otherwise one
-// workgroup per item.  With `chosen`, nothing is launched: the schedule is stored there instead.
+// when asked for, or, by default, when the items exceed what the device holds at once and partitions
+// hold at least kQueueMinPartitionTokens tokens; otherwise one workgroup per item.  With `chosen`, nothing is launched: the schedule is stored there instead.
 template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP>
 hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedule, bool queue_ok, hipStream_t stream,
                                    int* chosen) {
@@ -1400,7 +1475,8 @@ hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedul
       int64_t capacity = 0;
       const hipError_t err = queue_capacity<E, D, GC, UB, AP>(&capacity);
       if (err != hipSuccess) return err;
-      if (schedule == kScheduleQueue || items > capacity) {
+      if (schedule == kScheduleQueue ||
+          (schedule == kScheduleAuto && items > capacity && prm.partition_tokens >= kQueueMinPartitionTokens)) {
         if (chosen != nullptr) {
           *chosen = RK_PA_SCHEDULE_QUEUE;
           return hipSuccess;
@@ -1796,6 +1872,7 @@ extern "C" int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t
   const int64_t items = batch * kv_heads * ((group + gc - 1) / gc) * s.num_partitions;
   Params prm{};
   prm.bs_log2 = log2_exact(block_size);
+  prm.partition_tokens = static_cast<int32_t>(partition_tokens);
   int chosen = RK_PA_SCHEDULE_GRID;
   const Launch l{items, requested, queue, nullptr, &chosen};
   const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(prm, head_dim, gc, variant, l, true, false)

@@ -210,3 +210,7 @@ def test_schedule_query_names_what_runs(gpu, palib):
         if partition < w.max_blocks * w.block_size:  # split-K: the queue can be forced
             assert palib.schedule(*args, schedule="queue") == "queue"
     assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 2048, variant="valu") == "grid"
+    # Partitions under 256 tokens keep the grid by default (the queue can still be forced).
+    assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 128) == "grid"
+    assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 128, schedule="queue") == "queue"
+    assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 256) == "queue"

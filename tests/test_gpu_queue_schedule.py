@@ -214,3 +214,38 @@ def test_schedule_query_names_what_runs(gpu, palib):
     assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 128) == "grid"
     assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 128, schedule="queue") == "queue"
     assert palib.schedule(128, 32, 8, 128, 16, 1024, "bf16", 256) == "queue"
+
+
+def test_queue_under_graph_capture_replays_match_eager(gpu, palib):
+    """The public call on a queue-scheduled shape, captured into a HIP graph: the capture takes the
+    two-launch form, whose ticket counter a one-thread kernel zeroes in front of every replay."""
+
+    import torch
+
+    import radeon_kernels as rk
+
+    batch, limit, bs = 48, 2048, 16
+    case = make_case(torch, batch=batch, query_heads=32, kv_heads=8, head_dim=128, block_size=bs,
+                     contexts=ragged_contexts(batch, limit, seed=31), max_blocks=limit // bs, seed=9)
+    dev = to_device(case, gpu)
+    args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    announce("queue graph capture")
+    eager = rk.paged_attention_decode(*args)
+    record = rk.get_last_dispatch()
+    partition = int(record["launch"]["partition_tokens"])
+    assert palib.schedule(batch, 32, 8, 128, bs, limit // bs, "bf16", partition) == "queue", record["launch"]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            rk.paged_attention_decode(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = rk.paged_attention_decode(*args)
+    for _ in range(3):
+        scratch = torch.randn(1 << 20, device=gpu)  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert same_bits(captured, eager)
+        del scratch

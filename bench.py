@@ -27,7 +27,8 @@ Prints one JSON line:
                    cores over a bounded sample of the same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5] [--variant mfma]
-                       [--partition P] [--merge fused|reduce] [--no-breakdown] [--no-cpu-baseline]
+                       [--partition P] [--merge fused|reduce] [--schedule auto|grid|queue]
+                       [--no-breakdown] [--no-cpu-baseline]
                        [--cpu-seconds S] [--calibration-copy]
        python bench.py --operator kv_cache_append|kv_cache_copy [--case ...] [--dtype bf16]
                        (the paged-cache operators around the decode; same JSON line shape)
@@ -69,6 +70,8 @@ def parse_args(argv=None):
     parser.add_argument("--partition", type=int, default=None)
     parser.add_argument("--merge", default=None, choices=["fused", "reduce"],
                         help="partition-record merge form (default: the workload's dispatch entry)")
+    parser.add_argument("--schedule", default="auto", choices=["auto", "grid", "queue"],
+                        help="partition-kernel schedule (default: the library's choice)")
     parser.add_argument("--no-breakdown", action="store_true",
                         help="time only the headline call (no per-kernel breakdown of the other form)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -615,7 +618,7 @@ def main(argv=None) -> int:
     counters = torch.zeros(lib.counter_words(batch, hq, hkv), dtype=torch.int32, device=device)
     stream = torch.cuda.current_stream(device)
     headline = "fused" if merge == "fused" else "all"
-    schedule = lib.schedule(batch, hq, hkv, d, bs, mb, w.dtype, partition, variant)
+    schedule = lib.schedule(batch, hq, hkv, d, bs, mb, w.dtype, partition, variant, schedule=args.schedule)
     partition_kernel = "pa_partition_queue_kernel" if schedule == "queue" else "pa_partition_kernel"
 
     # Every launch's ctypes arguments are built once, so a timed loop makes one foreign call per
@@ -627,7 +630,7 @@ def main(argv=None) -> int:
             if (phase, copy) not in prepared:
                 prepared[phase, copy] = lib.prepare(q, k, v, bt, cl, partition_tokens=partition, variant=variant,
                                                     out=out, workspace=workspace, stream=stream, phase=phase,
-                                                    counters=counters)
+                                                    counters=counters, schedule=args.schedule)
 
     def launch(phase: str, copy: int) -> None:
         prepared[phase, copy]()
@@ -709,7 +712,7 @@ def main(argv=None) -> int:
         appends = [kvlib.prepare_append(new_k, new_v, kc, vc, slots, stream=stream) for kc, vc in caches]
         fused_steps = [lib.prepare(q, kc, vc, bt, cl, partition_tokens=partition, variant=variant, out=out,
                                    workspace=workspace, stream=stream, phase=headline, counters=counters,
-                                   new_key=new_k, new_value=new_v) for kc, vc in caches]
+                                   new_key=new_k, new_value=new_v, schedule=args.schedule) for kc, vc in caches]
 
         def step_us(one_step) -> float:
             for i in range(args.warmup):

@@ -92,6 +92,21 @@ extern "C" {
 #define RK_PA_SCHEDULE_QUEUE 0x200
 
 /*
+ * Partition growth, OR-ed into the variant argument (no reference counterpart): partition_tokens
+ * becomes the smallest partition size.  When the work-queue schedule runs, its workgroups read the
+ * context lengths and run partitions of P = partition_tokens * 2^k tokens, the largest k with
+ * P^2 <= 1440 * W (W: the context tokens of all sequences, each clamped to the table, times the
+ * head slots per sequence -- KV heads x head chunks -- divided by the workgroups of the launch),
+ * within 4096 tokens, 256 blocks and fewer tokens than the table holds
+ * (max_blocks_per_sequence * block_size).  Without the work queue
+ * the bit changes nothing.  Records keep the layout of partition_tokens, so the workspace size is
+ * unchanged; the two-launch forms keep the size the partition launch ran in workspace header word 1
+ * for the reduce launch, so rk_pa_decode_partitions and rk_pa_decode_reduce take the same variant.
+ * The output is bit-identical to a call without the bit at partition_tokens * 2^k.
+ */
+#define RK_PA_PARTITION_GROW 0x400
+
+/*
  * The schedule (RK_PA_SCHEDULE_GRID or RK_PA_SCHEDULE_QUEUE) that rk_pa_decode, its phase entries,
  * rk_pa_decode_fused and rk_pa_decode_noalloc run for these arguments on the current device (no
  * reference counterpart).  The index dtype does not enter the choice.  Launches nothing; the first
@@ -103,7 +118,8 @@ int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t kv_heads, 
 
 /*
  * Bytes of device workspace rk_pa_decode needs for this shape and partition size: a 256-byte
- * header (the work-queue ticket counter) and the split-K partial (max, sum, accumulator) records,
+ * header (word 0: the work-queue ticket counter; word 1: the partition size a growing call ran) and
+ * the split-K partial (max, sum, accumulator) records,
  * fp32.  Zero when one partition covers max_blocks_per_sequence * block_size tokens (the
  * single-pass launch needs none).
  */
@@ -116,7 +132,8 @@ int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t hea
  *
  * partition_tokens: context tokens per workgroup (split-K partition); a multiple of 16 in
  *   [16, 8192] with partition_tokens / block_size <= 256.
- * variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_VALU, optionally OR-ed with one RK_PA_SCHEDULE_* bit.
+ * variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_VALU, optionally OR-ed with one RK_PA_SCHEDULE_* bit
+ *   and with RK_PA_PARTITION_GROW.
  * workspace/workspace_bytes: device buffer of at least rk_pa_decode_workspace_bytes(...) bytes
  *   (may be NULL/0 when that is zero).  Its contents need no initialisation.
  * stream: hipStream_t to launch on (NULL = the null stream).

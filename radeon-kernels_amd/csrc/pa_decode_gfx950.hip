@@ -60,6 +60,15 @@ constexpr int kQueueMaxLevels = 256;
 // 1113 us).
 constexpr int kQueueMinPartitionTokens = 256;
 constexpr size_t kQueueHeaderBytes = 256;  // workspace bytes in front of the split-K records
+// Partition growth (RK_PA_PARTITION_GROW): the queue kernel doubles the partition size P while
+// P^2 <= kGrowBalance * W, W = context tokens x head slots per resident workgroup, up to
+// kGrowMaxTokens.  Each item costs a fixed prologue and epilogue and the last items to finish set a
+// tail of about one item, so the best size grows as sqrt(W).  Over eleven batches (16-1024 sequences
+// of 1 to 64k tokens) the fastest of the fixed sizes 256-4096 bounds the constant to [1350, 1531);
+// inside it the rule picks that size on all eleven.
+constexpr int64_t kGrowBalance = 1440;
+constexpr int kGrowMaxTokens = 4096;
+constexpr int kGrowMaxSteps = 8;  // 16 << 8 = 4096
 constexpr float kLog2e = 1.4426950408889634f;
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory operations are
 // outstanding: vmcnt in bits [3:0] and [15:14], expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait on
@@ -299,6 +308,12 @@ struct Params {
   // their exits on it and the last one zeroes both words for the next call.
   uint32_t* __restrict__ queue;
   uint32_t* __restrict__ queue_done;
+  // Partition growth (work-queue schedule with RK_PA_PARTITION_GROW only; else null / 0): the queue
+  // kernel runs partitions of partition_tokens << k tokens, at most grow_max_tokens, k chosen from
+  // the context lengths.  grown: two-launch form only, workspace header word 1, where workgroup 0
+  // stores the partition size it ran for the reduce kernel.
+  uint32_t* __restrict__ grown;
+  int32_t grow_max_tokens;
 };
 
 __device__ __forceinline__ int64_t clamped_context(const Params& p, int b) {
@@ -423,7 +438,14 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
   const int b = static_cast<int>(row / p.query_heads);
   const int64_t ctx = clamped_context(p, b);
   if (ctx <= 0) return;  // written by the partition kernel
-  const int np = static_cast<int>((ctx + p.partition_tokens - 1) / p.partition_tokens);
+  // The partition size the queue kernel ran; a stored value outside [partition_tokens,
+  // grow_max_tokens] is not one it can run, and the call's own size keeps the reads in the records.
+  int P = p.partition_tokens;
+  if (p.grown != nullptr) {
+    const int g = static_cast<int>(*p.grown);
+    if (g > P && g <= p.grow_max_tokens) P = g;
+  }
+  const int np = static_cast<int>((ctx + P - 1) / P);
   if (np <= 1) return;   // written by the partition kernel
   merge_partitions<E, D, false>(p, row, np, lane);
 }
@@ -459,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
 // partition past it); memory operations it issues are waited for only where their results are used.
 template <class E, int D, int GC, bool QK_MFMA, bool UB, bool AP, class Epilogue>
 __device__ __attribute__((always_inline)) inline void partition_item(const Params& p, const int tid, int b, int hslot,
-                                                                     int part, Epilogue&& at_epilogue) {
+                                                                     int part, const int P, Epilogue&& at_epilogue) {
   static_assert(!AP || QK_MFMA, "append-and-decode is built for the MFMA variant");
   constexpr int KSTEPS = D / 32;       // MFMA k-steps; also DMA instructions per K tile
   constexpr int VEC = D / 16;          // elements of a token row per lane (row = 16 lanes)
@@ -512,7 +534,6 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   // itself, this partition's block-table slice, the query and (uniform-block path) the block ids of
   // the wave's first tiles -- is issued together, so the workgroup waits one memory latency, not
   // three, before it sends out its first K/V loads.
-  const int P = p.partition_tokens;
   const int lb = p.bs_log2;
   const int bs_mask = (1 << lb) - 1;
   const int p0 = part * P;
@@ -1070,7 +1091,8 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   const int64_t rest = wg / heads_per_seq;
   const int b = static_cast<int>(rest % p.batch);
   const int part = static_cast<int>(rest / p.batch);
-  partition_item<E, D, GC, QK_MFMA, UB, AP>(p, static_cast<int>(threadIdx.x), b, hslot, part, [] {});
+  partition_item<E, D, GC, QK_MFMA, UB, AP>(p, static_cast<int>(threadIdx.x), b, hslot, part, p.partition_tokens,
+                                            [] {});
 }
 
 // Item-map helpers of the work-queue kernel.  kQueueBins counts the key values of its two sorts: a
@@ -1157,7 +1179,8 @@ __device__ __attribute__((always_inline)) inline int queue_sort(int batch, int t
 // for every item past its sequence's context (3672 of its 8192 items, about 4 us each); here only
 // items with tokens are scheduled.
 //
-// Item map, built by every workgroup from the context lengths alone, so all agree on it.  A
+// Item map, built by every workgroup from the context lengths alone, so all agree on it (P is the
+// call's partition size, or the size partition growth picks, also from the contexts alone).  A
 // sequence with c > 0 tokens (clamped to the table) has f = c / P full partitions and, when P does
 // not divide c, one partial partition of c % P tokens; a context <= 0 has one partial partition of
 // no tokens (its item writes the NaN row).  Items are numbered largest first: the full partitions
@@ -1191,18 +1214,62 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
   const int heads_per_seq = p.kv_heads * p.head_chunks;
   const bool is64 = p.index_is64 != 0;
   const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << p.bs_log2;
-  const int P = p.partition_tokens;
+  __shared__ unsigned long long s_tokens;
+
+  // This thread's sequences (tid + r * kThreads; the host admits at most kQueueMaxBatch) and their
+  // context lengths clamped to the table, loaded once for the partition size and the item map.
+  constexpr int kSeqPerThread = kQueueMaxBatch / kThreads;
+  int cc_own[kSeqPerThread];
+#pragma unroll
+  for (int r = 0; r < kSeqPerThread; ++r) {
+    const int i = tid + r * kThreads;
+    cc_own[r] = 0;
+    if (i < p.batch) {
+      const int64_t c = index_value(load_raw_index(p.context_lengths, i, is64), is64);
+      cc_own[r] = static_cast<int>(c < max_ctx ? c : max_ctx);
+    }
+  }
+
+  // Partition growth: the largest P << k within the host's limit with (P << k)^2 <= kGrowBalance *
+  // W, W = context tokens x head slots per resident workgroup, from the same clamped contexts as the
+  // item map, so every workgroup picks the same size.
+  int P = p.partition_tokens;
+  if (p.grow_max_tokens > P) {
+    if (tid == 0) s_tokens = 0;
+    __syncthreads();
+    unsigned long long own = 0;
+#pragma unroll
+    for (int r = 0; r < kSeqPerThread; ++r) own += cc_own[r] > 0 ? static_cast<unsigned long long>(cc_own[r]) : 0ull;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) own += __shfl_xor(own, off);
+    if (lane == 0) atomicAdd(&s_tokens, own);
+    __syncthreads();
+    const int64_t tokens = static_cast<int64_t>(s_tokens);  // <= 1024 * 2^31
+    const int64_t work = min(tokens * heads_per_seq / static_cast<int64_t>(gridDim.x), int64_t{1} << 40);
+    int grow = 0;
+    for (int k = 1; k <= kGrowMaxSteps; ++k) {
+      const int64_t next = static_cast<int64_t>(P) << k;
+      if (next > p.grow_max_tokens || next * next > kGrowBalance * work) break;
+      grow = k;
+    }
+    P = __builtin_amdgcn_readfirstlane(P << grow);
+    if (p.grown != nullptr && blockIdx.x == 0 && tid == 0)
+      __hip_atomic_store(p.grown, static_cast<uint32_t>(P), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   if (tid == 0) {
     s_levels = 0;
     s_partials = 0;
   }
-  for (int i = tid; i < p.batch; i += kThreads) {
-    const int64_t c = index_value(load_raw_index(p.context_lengths, i, is64), is64);
-    const int cc = static_cast<int>(c < max_ctx ? c : max_ctx);
-    const int rem = cc <= 0 ? 0 : cc % P;
-    s_full[i] = static_cast<uint16_t>(cc <= 0 ? 0 : cc / P);
-    s_class[i] = static_cast<int16_t>(cc > 0 && rem == 0 ? -1 : (rem + kQueueClassTokens - 1) / kQueueClassTokens);
+#pragma unroll
+  for (int r = 0; r < kSeqPerThread; ++r) {
+    const int i = tid + r * kThreads;
+    if (i < p.batch) {
+      const int cc = cc_own[r];
+      const int rem = cc <= 0 ? 0 : cc % P;
+      s_full[i] = static_cast<uint16_t>(cc <= 0 ? 0 : cc / P);
+      s_class[i] = static_cast<int16_t>(cc > 0 && rem == 0 ? -1 : (rem + kQueueClassTokens - 1) / kQueueClassTokens);
+    }
   }
   __syncthreads();
   // Full order.  Before its rounds the bins hold, for level k, the number of sequences with more than
@@ -1296,7 +1363,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
     // through every item's epilogue (hoisted, they took the 128-dim GQA-4 form to one wave per SIMD).
     int item_tid = tid;
     __asm__ volatile("" : "+v"(item_tid));
-    partition_item<E, D, GC, true, UB, AP>(p, item_tid, b, hslot, part, [&]() __attribute__((always_inline)) {
+    partition_item<E, D, GC, true, UB, AP>(p, item_tid, b, hslot, part, P, [&]() __attribute__((always_inline)) {
       if (tid == 0) {
         claimed = ticket();
         has_claim = true;
@@ -1390,7 +1457,8 @@ int64_t partitions_for(const Shape& s) {
   return (s.max_blocks * s.block_size + s.partition - 1) / s.partition;
 }
 
-// Workspace layout: a 256-byte header (word 0: the work-queue ticket counter), partition
+// Workspace layout: a 256-byte header (word 0: the work-queue ticket counter; word 1: the partition
+// size a growing queue launch ran, for the reduce kernel), partition
 // accumulators (fp32, padded to 256 B), then partition (max, sum) pairs.
 size_t acc_bytes_for(const Shape& s) {
   const size_t records = static_cast<size_t>(s.batch) * s.query_heads * s.num_partitions;
@@ -1631,17 +1699,32 @@ constexpr int kPhaseAppend = 8; // partition kernel also writes each sequence's 
 constexpr int kPhaseScratch = 16; // records in this device's `scratch` array, not `workspace`
 
 // The variant argument's kernel variant (low byte) and RK_PA_SCHEDULE_* request.
-int split_variant(int* variant, int* schedule) {
+int split_variant(int* variant, int* schedule, bool* grow = nullptr) {
   const int bits = *variant;
-  if ((bits & ~(RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE | 0xFF)) != 0 ||
+  if ((bits & ~(RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE | RK_PA_PARTITION_GROW | 0xFF)) != 0 ||
       (bits & (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE)) == (RK_PA_SCHEDULE_GRID | RK_PA_SCHEDULE_QUEUE) ||
       ((bits & 0xFF) != RK_PA_VARIANT_MFMA && (bits & 0xFF) != RK_PA_VARIANT_VALU))
     return fail(RK_ERR_INVALID_ARGUMENT, "unknown kernel variant %d", bits);
   *schedule = (bits & RK_PA_SCHEDULE_QUEUE) != 0 ? kScheduleQueue
               : (bits & RK_PA_SCHEDULE_GRID) != 0 ? kScheduleGrid
                                                   : kScheduleAuto;
+  if (grow != nullptr) *grow = (bits & RK_PA_PARTITION_GROW) != 0;
   *variant = bits & 0xFF;
   return RK_OK;
+}
+
+// Largest partition size partition growth may reach: partition_tokens doubled while it stays within
+// kGrowMaxTokens and 256 blocks and leaves the table at least two partitions; 0 when no doubling
+// fits.
+int32_t grow_limit(const Shape& s) {
+  const int64_t table_tokens = s.max_blocks * s.block_size;
+  int64_t limit = s.partition;
+  for (int k = 0; k < kGrowMaxSteps; ++k) {
+    const int64_t next = limit * 2;
+    if (next > kGrowMaxTokens || next / s.block_size > kMaxSliceBlocks - 1 || next >= table_tokens) break;
+    limit = next;
+  }
+  return limit > s.partition ? static_cast<int32_t>(limit) : 0;
 }
 
 int decode_phases(const void* query, const void* key_cache, const void* value_cache,
@@ -1666,7 +1749,8 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   if (index_dtype != RK_INDEX_INT32 && index_dtype != RK_INDEX_INT64)
     return fail(RK_ERR_INVALID_ARGUMENT, "index_dtype must be RK_INDEX_INT32 or RK_INDEX_INT64");
   int schedule = kScheduleAuto;
-  if (split_variant(&variant, &schedule) != RK_OK) return RK_ERR_INVALID_ARGUMENT;
+  bool grow = false;
+  if (split_variant(&variant, &schedule, &grow) != RK_OK) return RK_ERR_INVALID_ARGUMENT;
   if (!(scale > 0.0f) || !isfinite(scale))
     return fail(RK_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
   if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(output))
@@ -1756,6 +1840,24 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.num_partitions = static_cast<int32_t>(s.num_partitions);
   prm.index_is64 = index_dtype == RK_INDEX_INT64 ? 1 : 0;
   prm.scale_log2e = scale * kLog2e;
+
+  // Partition growth runs on the work-queue schedule only.  The dry run makes the partition launch's
+  // own choice, also in a reduce-only call, which must read the size that launch ran.
+  if (grow && schedule != kScheduleGrid && queue_eligible(s, variant)) {
+    const int32_t limit = grow_limit(s);
+    if (limit > 0) {
+      int chosen = RK_PA_SCHEDULE_GRID;
+      const Launch dry{grid, schedule, true, nullptr, &chosen};
+      const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(prm, head_dim, gc, variant, dry, true, false)
+                                                    : launch_dtype<Fp16>(prm, head_dim, gc, variant, dry, true, false);
+      if (err != hipSuccess)
+        return fail(RK_ERR_LAUNCH, "paged attention schedule query failed: %s", hipGetErrorString(err));
+      if (chosen == RK_PA_SCHEDULE_QUEUE) {
+        prm.grow_max_tokens = limit;
+        if (!fused) prm.grown = static_cast<uint32_t*>(workspace) + 1;  // header word 1
+      }
+    }
+  }
 
   const bool reduce = !fused && (phases & kPhaseReduce) != 0 && s.num_partitions > 1;
   const Launch l{grid, schedule, queue, static_cast<hipStream_t>(stream), nullptr};

@@ -20,6 +20,10 @@
 // for the next call on that stream.  Calls made while the stream is being captured into a graph
 // always use the two-launch form, which needs no state that outlives the call.
 //
+// The launch parameter `grow_partitions` (default false) sets RK_PA_PARTITION_GROW: partition_tokens
+// is then the smallest partition size, and on the work-queue schedule the kernel doubles it while
+// its square stays within 1440 times the context tokens per workgroup, from the live context lengths.
+//
 // decode_append_mfma (no reference counterpart) is one serving step in the decode's launch: it
 // stores each sequence's new token (position context_length - 1) into the caches in place and
 // returns the decode of the updated context, bit-identical to kv_cache_append then decode_mfma.
@@ -197,20 +201,22 @@ at::Tensor decode(const at::Tensor& query, const at::Tensor& key_cache,
   return output;
 }
 
+int grow_bits(bool grow_partitions) { return grow_partitions ? RK_PA_PARTITION_GROW : 0; }
+
 at::Tensor decode_mfma(const at::Tensor& query, const at::Tensor& key_cache,
                        const at::Tensor& value_cache, const at::Tensor& block_tables,
                        const at::Tensor& context_lengths, double scale, int64_t partition_tokens,
-                       const std::string& merge) {
+                       const std::string& merge, bool grow_partitions) {
   return decode(query, key_cache, value_cache, block_tables, context_lengths, scale,
-                partition_tokens, merge, RK_PA_VARIANT_MFMA);
+                partition_tokens, merge, RK_PA_VARIANT_MFMA | grow_bits(grow_partitions));
 }
 
 at::Tensor decode_valu(const at::Tensor& query, const at::Tensor& key_cache,
                        const at::Tensor& value_cache, const at::Tensor& block_tables,
                        const at::Tensor& context_lengths, double scale, int64_t partition_tokens,
-                       const std::string& merge) {
+                       const std::string& merge, bool grow_partitions) {
   return decode(query, key_cache, value_cache, block_tables, context_lengths, scale,
-                partition_tokens, merge, RK_PA_VARIANT_VALU);
+                partition_tokens, merge, RK_PA_VARIANT_VALU | grow_bits(grow_partitions));
 }
 
 // Append-and-decode: writes each sequence's new token into the caches (in place) and returns the
@@ -219,9 +225,9 @@ at::Tensor decode_append_mfma(const at::Tensor& query, const at::Tensor& new_key
                               const at::Tensor& new_value, const at::Tensor& key_cache,
                               const at::Tensor& value_cache, const at::Tensor& block_tables,
                               const at::Tensor& context_lengths, double scale, int64_t partition_tokens,
-                              const std::string& merge) {
+                              const std::string& merge, bool grow_partitions) {
   return decode(query, key_cache, value_cache, block_tables, context_lengths, scale, partition_tokens,
-                merge, RK_PA_VARIANT_MFMA, new_key, new_value);
+                merge, RK_PA_VARIANT_MFMA | grow_bits(grow_partitions), new_key, new_value);
 }
 
 }  // namespace
@@ -231,15 +237,18 @@ PYBIND11_MODULE(rk_pa_gfx950, module) {
   module.def("decode_mfma", &decode_mfma, "paged decode, QK^T on MFMA", py::arg("query"),
              py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
              py::arg("context_lengths"), py::arg("scale"), py::kw_only(),
-             py::arg("partition_tokens") = 512, py::arg("merge") = "auto");
+             py::arg("partition_tokens") = 512, py::arg("merge") = "auto",
+             py::arg("grow_partitions") = false);
   module.def("decode_append_mfma", &decode_append_mfma,
              "append each sequence's new token to the paged caches, then paged decode (one launch)",
              py::arg("query"), py::arg("new_key"), py::arg("new_value"), py::arg("key_cache"),
              py::arg("value_cache"), py::arg("block_tables"), py::arg("context_lengths"), py::arg("scale"),
-             py::kw_only(), py::arg("partition_tokens") = 512, py::arg("merge") = "auto");
+             py::kw_only(), py::arg("partition_tokens") = 512, py::arg("merge") = "auto",
+             py::arg("grow_partitions") = false);
   module.def("decode_valu", &decode_valu, "paged decode, QK^T on fp32 FMAs", py::arg("query"),
              py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
              py::arg("context_lengths"), py::arg("scale"), py::kw_only(),
-             py::arg("partition_tokens") = 512, py::arg("merge") = "auto");
+             py::arg("partition_tokens") = 512, py::arg("merge") = "auto",
+             py::arg("grow_partitions") = false);
   module.def("version", []() { return std::string(rk_pa_version()); });
 }

@@ -33,6 +33,9 @@ VARIANTS = {"mfma": 0, "valu": 1}
 # Partition-kernel schedule bits OR-ed into the variant (RK_PA_SCHEDULE_*); "auto" lets the library
 # choose.
 SCHEDULES = {"auto": 0, "grid": 0x100, "queue": 0x200}
+# Partition growth (RK_PA_PARTITION_GROW): partition_tokens is the smallest partition size the
+# work-queue schedule runs.
+RK_PA_PARTITION_GROW = 0x400
 
 EXPORTED_SYMBOLS = (
     "rk_pa_decode",
@@ -48,6 +51,10 @@ EXPORTED_SYMBOLS = (
     "rk_pa_version",
 )
 PHASES = {"all": "rk_pa_decode", "partitions": "rk_pa_decode_partitions", "reduce": "rk_pa_decode_reduce"}
+
+
+def _variant_bits(variant: str, schedule: str, grow: bool) -> int:
+    return VARIANTS[variant] | SCHEDULES[schedule] | (RK_PA_PARTITION_GROW if grow else 0)
 
 
 def _repeatable(function: Any, args: tuple[Any, ...], check: Any, held: tuple[Any, ...]) -> Any:
@@ -177,7 +184,7 @@ class PagedAttentionLibrary:
 
     def decode_noalloc(self, query: Any, key_cache: Any, value_cache: Any, block_tables: Any, context_lengths: Any,
                        scale: float | None = None, *, out: Any, partition_tokens: int = 512, variant: str = "mfma",
-                       stream: Any | None = None, schedule: str = "auto") -> Any:
+                       stream: Any | None = None, schedule: str = "auto", grow: bool = False) -> Any:
         """rk_pa_decode_noalloc on torch tensors: writes ``out`` (caller-allocated) and returns it.
 
         The split-K records live in the library's per-GPU scratch array, so nothing is allocated
@@ -199,7 +206,7 @@ class PagedAttentionLibrary:
             block_size=block_size, max_blocks=int(block_tables.shape[1]), scale=float(scale),
             dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
             index_dtype=RK_INDEX_INT64 if block_tables.dtype == torch.int64 else RK_INDEX_INT32,
-            partition_tokens=partition_tokens, variant=VARIANTS[variant] | SCHEDULES[schedule],
+            partition_tokens=partition_tokens, variant=_variant_bits(variant, schedule, grow),
             stream=stream.cuda_stream))
         return out
 
@@ -213,7 +220,7 @@ class PagedAttentionLibrary:
                      scale: float | None, partition_tokens: int, variant: str, out: Any | None,
                      workspace: Any | None, stream: Any | None, phase: str, counters: Any | None,
                      new_key: Any | None = None, new_value: Any | None = None,
-                     schedule: str = "auto") -> tuple[Any, Any, tuple[Any, ...], tuple[Any, ...]]:
+                     schedule: str = "auto", grow: bool = False) -> tuple[Any, Any, tuple[Any, ...], tuple[Any, ...]]:
         """(out, C function, its arguments, tensors those arguments point into)."""
 
         import torch
@@ -241,7 +248,7 @@ class PagedAttentionLibrary:
             block_size=block_size, max_blocks=max_blocks, scale=float(scale),
             dtype=RK_DTYPE_BF16 if query.dtype == torch.bfloat16 else RK_DTYPE_FP16,
             index_dtype=RK_INDEX_INT64 if block_tables.dtype == torch.int64 else RK_INDEX_INT32,
-            partition_tokens=partition_tokens, variant=VARIANTS[variant] | SCHEDULES[schedule],
+            partition_tokens=partition_tokens, variant=_variant_bits(variant, schedule, grow),
             stream=stream.cuda_stream, phase=phase,
             counters=counters.data_ptr() if counters is not None else 0,
             counter_words=counters.numel() if counters is not None else 0,
@@ -256,18 +263,19 @@ class PagedAttentionLibrary:
                scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
                out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
                phase: str = "all", counters: Any | None = None, new_key: Any | None = None,
-               new_value: Any | None = None, schedule: str = "auto") -> Any:
+               new_value: Any | None = None, schedule: str = "auto", grow: bool = False) -> Any:
         """Launch on torch tensors (all on one GPU); returns ``out`` (allocated if None).
 
         ``counters`` (phase ``"fused"`` only): an int32 tensor of at least ``counter_words`` zeros,
         allocated zeroed here if None.  ``new_key`` / ``new_value`` ([batch, kv_heads, head_dim]):
         append-and-decode (rk_pa_decode_append), which also writes them into the caches.
-        ``schedule``: ``"auto"``, ``"grid"`` or ``"queue"`` (the RK_PA_SCHEDULE_* bits).
+        ``schedule``: ``"auto"``, ``"grid"`` or ``"queue"`` (the RK_PA_SCHEDULE_* bits); ``grow``:
+        partition growth (RK_PA_PARTITION_GROW).
         """
 
         out, function, args, _ = self._tensor_call(query, key_cache, value_cache, block_tables, context_lengths,
                                                    scale, partition_tokens, variant, out, workspace, stream, phase,
-                                                   counters, new_key, new_value, schedule)
+                                                   counters, new_key, new_value, schedule, grow)
         self.check(function(*args))
         return out
 
@@ -275,7 +283,7 @@ class PagedAttentionLibrary:
                 scale: float | None = None, *, partition_tokens: int = 512, variant: str = "mfma",
                 out: Any | None = None, workspace: Any | None = None, stream: Any | None = None,
                 phase: str = "all", counters: Any | None = None, new_key: Any | None = None,
-                new_value: Any | None = None, schedule: str = "auto") -> Any:
+                new_value: Any | None = None, schedule: str = "auto", grow: bool = False) -> Any:
         """The launch ``decode`` would make, with every argument converted once.
 
         Returns a zero-argument callable that repeats it (one foreign call per launch, no Python
@@ -285,7 +293,7 @@ class PagedAttentionLibrary:
 
         _, function, args, held = self._tensor_call(query, key_cache, value_cache, block_tables, context_lengths,
                                                     scale, partition_tokens, variant, out, workspace, stream,
-                                                    phase, counters, new_key, new_value, schedule)
+                                                    phase, counters, new_key, new_value, schedule, grow)
         return _repeatable(function, args, self.check, held)
 
 

@@ -73,6 +73,7 @@ def test_status_codes_match_header():
                              "valu": int(re.search(r"RK_PA_VARIANT_VALU (\d+)", text).group(1))}
     assert cabi.SCHEDULES == {"auto": 0, "grid": int(re.search(r"RK_PA_SCHEDULE_GRID (0x[0-9a-f]+)", text).group(1), 16),
                               "queue": int(re.search(r"RK_PA_SCHEDULE_QUEUE (0x[0-9a-f]+)", text).group(1), 16)}
+    assert cabi.RK_PA_PARTITION_GROW == int(re.search(r"RK_PA_PARTITION_GROW (0x[0-9a-f]+)", text).group(1), 16)
 
 
 def expected_workspace(batch, hq, d, bs, mb, partition):
@@ -139,7 +140,14 @@ def call(lib, **overrides):
         # Schedule bits: both at once, or an unknown bit, are invalid; the queue needs the MFMA variant,
         # a split-K shape (several partitions), at most 256 partitions and at most 1024 sequences.
         (dict(variant=0x300), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
-        (dict(variant=0x400), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        (dict(variant=0x800), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        (dict(variant=0x700), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
+        # Partition growth combines with either schedule and either variant; a forced queue still
+        # needs an eligible shape, and the workspace is that of partition_tokens.
+        (dict(variant=0x600), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
+        (dict(variant=0x401, max_blocks=64), cabi.RK_ERR_WORKSPACE, "workspace of"),
+        (dict(variant=0x500, max_blocks=64, workspace=1 << 20, workspace_bytes=100), cabi.RK_ERR_WORKSPACE,
+         "workspace of"),
         (dict(variant=0x201, max_blocks=64, workspace=1 << 20, workspace_bytes=1 << 20), cabi.RK_ERR_UNSUPPORTED,
          "work-queue schedule"),
         (dict(variant=0x200), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
@@ -165,6 +173,8 @@ def test_invalid_arguments_are_rejected_before_launch(lib, overrides, status, me
         (dict(head_dim=96), cabi.RK_ERR_INVALID_ARGUMENT, "one of 64, 128, 256"),
         (dict(variant=0x200, max_blocks=4), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
         (dict(variant=0x201), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
+        (dict(variant=0x601), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
+        (dict(variant=0xB00), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
     ],
 )
 def test_schedule_query_validates_before_asking_the_device(lib, overrides, status, message):

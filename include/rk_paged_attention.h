@@ -98,9 +98,11 @@ extern "C" {
  * P^2 <= 1440 * W (W: the context tokens of all sequences, each clamped to the table, times the
  * head slots per sequence -- KV heads x head chunks -- divided by the workgroups of the launch),
  * within 4096 tokens, 256 blocks and fewer tokens than the table holds
- * (max_blocks_per_sequence * block_size).  Without the work queue
- * the bit changes nothing.  Records keep the layout of partition_tokens, so the workspace size is
- * unchanged; the two-launch forms keep the size the partition launch ran in workspace header word 1
+ * (max_blocks_per_sequence * block_size).  A table wider than 256 partitions of partition_tokens
+ * (too wide for the work queue) starts from the first doubling of partition_tokens that fits, if
+ * one does within those limits, so long tables also run on the work queue.  Without the work queue
+ * the bit changes nothing.  Records keep the layout of that smallest size, so the workspace
+ * rk_pa_decode_workspace_bytes gives for partition_tokens suffices; the two-launch forms keep the size the partition launch ran in workspace header word 1
  * for the reduce launch, so rk_pa_decode_partitions and rk_pa_decode_reduce take the same variant.
  * The output is bit-identical to a call without the bit at partition_tokens * 2^k.
  */

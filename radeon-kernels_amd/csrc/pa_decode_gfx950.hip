@@ -1713,6 +1713,24 @@ int split_variant(int* variant, int* schedule, bool* grow = nullptr) {
   return RK_OK;
 }
 
+// Partition growth's smallest size for a table too wide for the queue's item map at partition_tokens
+// (more than kQueueMaxLevels partitions): the first doubling that fits, within kGrowMaxTokens and 256
+// blocks.  The call then runs, and lays out its records, as if given that size; a call the queue
+// cannot take anyway (grid schedule requested, VALU variant, too many sequences) is left unchanged.
+void grow_base(Shape* s, int variant, int schedule, bool grow) {
+  if (!grow || schedule == kScheduleGrid || variant != RK_PA_VARIANT_MFMA || s->batch > kQueueMaxBatch ||
+      s->num_partitions <= kQueueMaxLevels)
+    return;
+  const int64_t table_tokens = s->max_blocks * s->block_size;
+  int64_t base = s->partition;
+  while ((table_tokens + base - 1) / base > kQueueMaxLevels) {
+    base *= 2;
+    if (base > kGrowMaxTokens || base / s->block_size > kMaxSliceBlocks - 1) return;
+  }
+  s->partition = base;
+  s->num_partitions = partitions_for(*s);
+}
+
 // Largest partition size partition growth may reach: partition_tokens doubled while it stays within
 // kGrowMaxTokens and 256 blocks and leaves the table at least two partitions; 0 when no doubling
 // fits.
@@ -1761,6 +1779,8 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   int status = check_shape(s);
   if (status != RK_OK) return status;
   s.num_partitions = partitions_for(s);
+  grow_base(&s, variant, schedule, grow);
+  partition_tokens = s.partition;
   const size_t need = workspace_for(s);
   if ((phases & kPhaseScratch) != 0) {
     if (need > RK_PA_NOALLOC_SCRATCH_BYTES)
@@ -1962,11 +1982,14 @@ extern "C" int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t
   if (dtype != RK_DTYPE_FP16 && dtype != RK_DTYPE_BF16)
     return fail(RK_ERR_INVALID_ARGUMENT, "dtype must be RK_DTYPE_FP16 or RK_DTYPE_BF16");
   int requested = kScheduleAuto;
-  if (split_variant(&variant, &requested) != RK_OK) return RK_ERR_INVALID_ARGUMENT;
+  bool grow = false;
+  if (split_variant(&variant, &requested, &grow) != RK_OK) return RK_ERR_INVALID_ARGUMENT;
   Shape s{batch, query_heads, kv_heads, head_dim, 1, block_size, max_blocks_per_sequence, partition_tokens, 0};
   const int status = check_shape(s);
   if (status != RK_OK) return status;
   s.num_partitions = partitions_for(s);
+  grow_base(&s, variant, requested, grow);
+  partition_tokens = s.partition;
   const bool queue = requested != kScheduleGrid && queue_eligible(s, variant);
   if (requested == kScheduleQueue && !queue) return queue_unsupported();
   const int64_t group = query_heads / kv_heads;

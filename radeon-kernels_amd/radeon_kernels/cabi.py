@@ -124,14 +124,14 @@ class PagedAttentionLibrary:
 
     def schedule(self, batch: int, query_heads: int, kv_heads: int, head_dim: int, block_size: int,
                  max_blocks: int, dtype: str, partition_tokens: int, variant: str = "mfma",
-                 schedule: str = "auto") -> str:
+                 schedule: str = "auto", grow: bool = False) -> str:
         """``"grid"`` or ``"queue"``: the partition-kernel schedule a decode with these arguments runs on
         the current device (rk_pa_decode_schedule)."""
 
         out = ctypes.c_int(0)
         self.check(self.lib.rk_pa_decode_schedule(batch, query_heads, kv_heads, head_dim, block_size, max_blocks,
                                                   RK_DTYPE_BF16 if dtype == "bf16" else RK_DTYPE_FP16,
-                                                  partition_tokens, VARIANTS[variant] | SCHEDULES[schedule],
+                                                  partition_tokens, _variant_bits(variant, schedule, grow),
                                                   ctypes.byref(out)))
         return {SCHEDULES["grid"]: "grid", SCHEDULES["queue"]: "queue"}[out.value]
 

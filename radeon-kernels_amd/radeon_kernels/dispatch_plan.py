@@ -125,7 +125,9 @@ BROAD_REGION: dict[str, Any] = {
 # Partitions of at least 256 tokens; on the work-queue schedule the kernel doubles them (up to 4096)
 # as the context tokens per workgroup allow, judged from the live context lengths, so a table sized
 # for long sequences does not coarsen the split of short ones.  On eleven batches of 16-1024
-# sequences of 1 to 64k tokens it ran the fastest fixed size, 21-37% faster than 256 tokens.
+# sequences of 1 to 64k tokens it ran the fastest fixed size, 21-37% faster than 256 tokens; a
+# 128k-token table (too wide for the queue at 256) starts from 512 on the queue and ran 1.5-5.9x
+# faster than the grid schedule at 256.
 BROAD_LAUNCH = {"partition_tokens": 256, "merge": "auto", "grow_partitions": True}
 
 _COMMON = {

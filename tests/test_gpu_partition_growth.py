@@ -155,6 +155,23 @@ def test_wide_table_with_short_contexts_keeps_the_base_size(gpu, palib):
     assert size == expected_size(contexts, 65536, 8, 256, 16, _capacity(gpu)) == 1024
 
 
+@pytest.mark.parametrize("batch, lo, hi", [(32, 1024, 3072), (8, 32768, 131072)])
+def test_table_too_wide_for_the_queue_starts_from_a_larger_size(gpu, palib, batch, lo, hi):
+    """A 128k-token table has 512 partitions of 256 tokens, more than the queue's item map holds:
+    without growth the call takes the grid schedule at 256; with growth it starts from 512 (256
+    partitions) on the work queue and grows from there."""
+
+    rng = random.Random(batch + lo)
+    contexts = [rng.randint(lo, hi) for _ in range(batch)]
+    announce(f"partition growth: 128k-token table, b{batch} {lo}-{hi} tokens")
+    assert palib.schedule(batch, 32, 8, 128, 16, 8192, "bf16", 256) == "grid"
+    assert palib.schedule(batch, 32, 8, 128, 16, 8192, "bf16", 256, grow=True) == "queue"
+    assert palib.schedule(batch, 32, 8, 128, 16, 8192, "bf16", 256, schedule="grid", grow=True) == "grid"
+    d = device_case(gpu, batch=batch, contexts=contexts, table_tokens=131072, seed=batch)
+    _, size = _check_against_fixed(palib, d, 256, f"128k table b{batch}")
+    assert size == expected_size(contexts, 131072, 8, 512, 16, _capacity(gpu)) > 512
+
+
 def test_growth_off_the_queue_changes_nothing(gpu, palib):
     """A grid-schedule shape: the bit changes nothing and header word 1 is not written."""
 

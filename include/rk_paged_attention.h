@@ -86,7 +86,9 @@ extern "C" {
  *                         rk_pa_decode_append, in the last two words of the counter array, which the
  *                         launch's last workgroup leaves zero (one launch).  Eligible: RK_PA_VARIANT_MFMA, a split-K shape
  *                         (rk_pa_decode_workspace_bytes > 0) with at most 256 partitions per
- *                         sequence and at most 1024 sequences; RK_ERR_UNSUPPORTED otherwise.
+ *                         sequence and at most 64512 sequences; RK_ERR_UNSUPPORTED otherwise.
+ * A batch of more than 1024 sequences on an eligible call runs as consecutive launches of 1024
+ * sequences (the last shorter) on the same stream, each choosing its own schedule.
  */
 #define RK_PA_SCHEDULE_GRID 0x100
 #define RK_PA_SCHEDULE_QUEUE 0x200
@@ -102,8 +104,10 @@ extern "C" {
  * (too wide for the work queue) starts from the first doubling of partition_tokens that fits, if
  * one does within those limits, so long tables also run on the work queue.  Without the work queue
  * the bit changes nothing.  Records keep the layout of that smallest size, so the workspace
- * rk_pa_decode_workspace_bytes gives for partition_tokens suffices; the two-launch forms keep the size the partition launch ran in workspace header word 1
- * for the reduce launch, so rk_pa_decode_partitions and rk_pa_decode_reduce take the same variant.
+ * rk_pa_decode_workspace_bytes gives for partition_tokens suffices.  The two-launch forms keep the
+ * size the partition launch ran in workspace header word 1 (word 1 + i for launch i of a batch of
+ * more than 1024 sequences) for the reduce launch, so rk_pa_decode_partitions and
+ * rk_pa_decode_reduce take the same variant.
  * The output is bit-identical to a call without the bit at partition_tokens * 2^k.
  */
 #define RK_PA_PARTITION_GROW 0x400
@@ -111,7 +115,7 @@ extern "C" {
 /*
  * The schedule (RK_PA_SCHEDULE_GRID or RK_PA_SCHEDULE_QUEUE) that rk_pa_decode, its phase entries,
  * rk_pa_decode_fused and rk_pa_decode_noalloc run for these arguments on the current device (no
- * reference counterpart).  The index dtype does not enter the choice.  Launches nothing; the first
+ * reference counterpart; for a batch run as launches of 1024 sequences, the first launch's).  The index dtype does not enter the choice.  Launches nothing; the first
  * query of a kernel configuration reads its occupancy from the runtime.
  */
 int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t kv_heads, int64_t head_dim,
@@ -120,7 +124,8 @@ int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t kv_heads, 
 
 /*
  * Bytes of device workspace rk_pa_decode needs for this shape and partition size: a 256-byte
- * header (word 0: the work-queue ticket counter; word 1: the partition size a growing call ran) and
+ * header (word 0: the work-queue ticket counter; words 1-63: the partition size each launch of a
+ * growing call ran) and
  * the split-K partial (max, sum, accumulator) records,
  * fp32.  Zero when one partition covers max_blocks_per_sequence * block_size tokens (the
  * single-pass launch needs none).

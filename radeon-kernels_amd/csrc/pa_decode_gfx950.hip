@@ -37,6 +37,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -53,6 +54,9 @@ constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, p
 // Work-queue schedule limits: sequences and partition levels whose item map fits in LDS.
 constexpr int kQueueMaxBatch = 1024;
 constexpr int kQueueMaxLevels = 256;
+// Larger batches run as launches of kQueueMaxBatch sequences; workspace header words 1 .. 63 hold the
+// partition size each launch ran under partition growth.
+constexpr int kQueueMaxLaunches = 63;
 // Smallest partition the automatic choice runs on the queue.  Below it items are a tile or two per
 // wave and the queue's per-item claim and barriers cost more than the grid's launches: 1024
 // sequences of 64-512 tokens at P 64 measured 654 against 629 us, of 64-1024 tokens at P 128 709
@@ -310,7 +314,7 @@ struct Params {
   uint32_t* __restrict__ queue_done;
   // Partition growth (work-queue schedule with RK_PA_PARTITION_GROW only; else null / 0): the queue
   // kernel runs partitions of partition_tokens << k tokens, at most grow_max_tokens, k chosen from
-  // the context lengths.  grown: two-launch form only, workspace header word 1, where workgroup 0
+  // the context lengths.  grown: two-launch form only, workspace header word 1 + launch, where workgroup 0
   // stores the partition size it ran for the reduce kernel.
   uint32_t* __restrict__ grown;
   int32_t grow_max_tokens;
@@ -1457,8 +1461,8 @@ int64_t partitions_for(const Shape& s) {
   return (s.max_blocks * s.block_size + s.partition - 1) / s.partition;
 }
 
-// Workspace layout: a 256-byte header (word 0: the work-queue ticket counter; word 1: the partition
-// size a growing queue launch ran, for the reduce kernel), partition
+// Workspace layout: a 256-byte header (word 0: the work-queue ticket counter; word 1 + i: the
+// partition size launch i of a growing call ran, for the reduce kernel), partition
 // accumulators (fp32, padded to 256 B), then partition (max, sum) pairs.
 size_t acc_bytes_for(const Shape& s) {
   const size_t records = static_cast<size_t>(s.batch) * s.query_heads * s.num_partitions;
@@ -1475,13 +1479,13 @@ size_t workspace_for(const Shape& s) {
 // the queue kernel's LDS; the VALU variant is not built for it.
 bool queue_eligible(const Shape& s, int variant) {
   return variant == RK_PA_VARIANT_MFMA && s.num_partitions > 1 && s.num_partitions <= kQueueMaxLevels &&
-         s.batch <= kQueueMaxBatch;
+         s.batch <= kQueueMaxBatch * kQueueMaxLaunches;
 }
 
 int queue_unsupported() {
   return fail(RK_ERR_UNSUPPORTED,
               "the work-queue schedule needs the MFMA variant, more than one partition per sequence "
-              "(at most %d) and at most %d sequences", kQueueMaxLevels, kQueueMaxBatch);
+              "(at most %d) and at most %d sequences", kQueueMaxLevels, kQueueMaxBatch * kQueueMaxLaunches);
 }
 
 // Counters of the fused launch: one 32-bit arrival counter per (sequence, KV head, head chunk), then
@@ -1718,7 +1722,8 @@ int split_variant(int* variant, int* schedule, bool* grow = nullptr) {
 // blocks.  The call then runs, and lays out its records, as if given that size; a call the queue
 // cannot take anyway (grid schedule requested, VALU variant, too many sequences) is left unchanged.
 void grow_base(Shape* s, int variant, int schedule, bool grow) {
-  if (!grow || schedule == kScheduleGrid || variant != RK_PA_VARIANT_MFMA || s->batch > kQueueMaxBatch ||
+  if (!grow || schedule == kScheduleGrid || variant != RK_PA_VARIANT_MFMA ||
+      s->batch > int64_t{kQueueMaxBatch} * kQueueMaxLaunches ||
       s->num_partitions <= kQueueMaxLevels)
     return;
   const int64_t table_tokens = s->max_blocks * s->block_size;
@@ -1831,7 +1836,14 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
     prm.ws_ml = reinterpret_cast<float*>(records + acc_bytes_for(s));
   }
   const bool partitions = (phases & (kPhasePartitions | kPhaseFused)) != 0;
-  const bool queue = partitions && schedule != kScheduleGrid && queue_eligible(s, variant);
+  // A batch larger than the queue's item map runs as launches of kQueueMaxBatch sequences (the last
+  // one shorter), in stream order on offset views of the same buffers.  Each picks its own schedule
+  // (and grown size), so every launch is a queue-eligible shape.
+  const int64_t rows_per_launch =
+      batch > kQueueMaxBatch && schedule != kScheduleGrid && queue_eligible(s, variant) ? kQueueMaxBatch : batch;
+  Shape first = s;
+  first.batch = rows_per_launch;
+  const bool queue = partitions && schedule != kScheduleGrid && queue_eligible(first, variant);
   if (partitions && schedule == kScheduleQueue && !queue) return queue_unsupported();
   if (queue && fused) {  // the ticket and exit counters after the arrival counters, zero on entry
     prm.queue = counters + arrival_words_for(batch, query_heads, kv_heads);
@@ -1848,7 +1860,6 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   }
   prm.block_stride = block_size * kv_heads * head_dim;
   prm.row_stride = kv_heads * head_dim;
-  prm.batch = static_cast<int32_t>(batch);
   prm.query_heads = static_cast<int32_t>(query_heads);
   prm.kv_heads = static_cast<int32_t>(kv_heads);
   prm.group = static_cast<int32_t>(group);
@@ -1861,30 +1872,55 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   prm.index_is64 = index_dtype == RK_INDEX_INT64 ? 1 : 0;
   prm.scale_log2e = scale * kLog2e;
 
-  // Partition growth runs on the work-queue schedule only.  The dry run makes the partition launch's
-  // own choice, also in a reduce-only call, which must read the size that launch ran.
-  if (grow && schedule != kScheduleGrid && queue_eligible(s, variant)) {
-    const int32_t limit = grow_limit(s);
-    if (limit > 0) {
-      int chosen = RK_PA_SCHEDULE_GRID;
-      const Launch dry{grid, schedule, true, nullptr, &chosen};
-      const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(prm, head_dim, gc, variant, dry, true, false)
-                                                    : launch_dtype<Fp16>(prm, head_dim, gc, variant, dry, true, false);
-      if (err != hipSuccess)
-        return fail(RK_ERR_LAUNCH, "paged attention schedule query failed: %s", hipGetErrorString(err));
-      if (chosen == RK_PA_SCHEDULE_QUEUE) {
-        prm.grow_max_tokens = limit;
-        if (!fused) prm.grown = static_cast<uint32_t*>(workspace) + 1;  // header word 1
+  const bool reduce = !fused && (phases & kPhaseReduce) != 0 && s.num_partitions > 1;
+  const int64_t index_bytes = index_dtype == RK_INDEX_INT64 ? 8 : 4;
+  const int64_t heads_per_seq = kv_heads * head_chunks;
+  for (int64_t launch = 0, b0 = 0; b0 < batch; ++launch, b0 += rows_per_launch) {
+    const int64_t rows = std::min(rows_per_launch, batch - b0);
+    Params cp = prm;
+    cp.batch = static_cast<int32_t>(rows);
+    cp.q = prm.q + b0 * query_heads * head_dim;
+    cp.out = prm.out + b0 * query_heads * head_dim;
+    cp.block_tables = static_cast<const char*>(block_tables) + b0 * max_blocks_per_sequence * index_bytes;
+    cp.context_lengths = static_cast<const char*>(context_lengths) + b0 * index_bytes;
+    if (need > 0) {
+      cp.ws_acc = prm.ws_acc + b0 * query_heads * s.num_partitions * head_dim;
+      cp.ws_ml = prm.ws_ml + b0 * query_heads * s.num_partitions * 2;
+    }
+    if (fused) cp.counters = counters + b0 * heads_per_seq;
+    if (append) {
+      cp.new_k = prm.new_k + b0 * kv_heads * head_dim;
+      cp.new_v = prm.new_v + b0 * kv_heads * head_dim;
+    }
+    const int64_t items = rows * heads_per_seq * s.num_partitions;
+    Shape sc = s;
+    sc.batch = rows;
+
+    // Partition growth runs on the work-queue schedule only.  The dry run makes the partition
+    // launch's own choice, also in a reduce-only call, which must read the size that launch ran
+    // (header word 1 + launch).
+    if (grow && schedule != kScheduleGrid && queue_eligible(sc, variant)) {
+      const int32_t limit = grow_limit(sc);
+      if (limit > 0) {
+        int chosen = RK_PA_SCHEDULE_GRID;
+        const Launch dry{items, schedule, true, nullptr, &chosen};
+        const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(cp, head_dim, gc, variant, dry, true, false)
+                                                      : launch_dtype<Fp16>(cp, head_dim, gc, variant, dry, true, false);
+        if (err != hipSuccess)
+          return fail(RK_ERR_LAUNCH, "paged attention schedule query failed: %s", hipGetErrorString(err));
+        if (chosen == RK_PA_SCHEDULE_QUEUE) {
+          cp.grow_max_tokens = limit;
+          if (!fused) cp.grown = static_cast<uint32_t*>(workspace) + 1 + launch;
+        }
       }
     }
-  }
 
-  const bool reduce = !fused && (phases & kPhaseReduce) != 0 && s.num_partitions > 1;
-  const Launch l{grid, schedule, queue, static_cast<hipStream_t>(stream), nullptr};
-  const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(prm, head_dim, gc, variant, l, partitions, reduce)
-                                                : launch_dtype<Fp16>(prm, head_dim, gc, variant, l, partitions, reduce);
-  if (err != hipSuccess)
-    return fail(RK_ERR_LAUNCH, "paged attention launch failed: %s", hipGetErrorString(err));
+    const Launch l{items, schedule, queue, static_cast<hipStream_t>(stream), nullptr};
+    const hipError_t err = dtype == RK_DTYPE_BF16 ? launch_dtype<Bf16>(cp, head_dim, gc, variant, l, partitions, reduce)
+                                                  : launch_dtype<Fp16>(cp, head_dim, gc, variant, l, partitions, reduce);
+    if (err != hipSuccess)
+      return fail(RK_ERR_LAUNCH, "paged attention launch failed: %s", hipGetErrorString(err));
+  }
   return RK_OK;
 }
 
@@ -1994,7 +2030,8 @@ extern "C" int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t
   if (requested == kScheduleQueue && !queue) return queue_unsupported();
   const int64_t group = query_heads / kv_heads;
   const int gc = head_chunk_for(group);
-  const int64_t items = batch * kv_heads * ((group + gc - 1) / gc) * s.num_partitions;
+  const int64_t rows = queue && batch > kQueueMaxBatch ? kQueueMaxBatch : batch;  // the first launch
+  const int64_t items = rows * kv_heads * ((group + gc - 1) / gc) * s.num_partitions;
   Params prm{};
   prm.bs_log2 = log2_exact(block_size);
   prm.partition_tokens = static_cast<int32_t>(partition_tokens);

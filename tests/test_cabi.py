@@ -138,7 +138,8 @@ def call(lib, **overrides):
         (dict(max_blocks=64, partition_tokens=64, workspace=4096 + 64, workspace_bytes=1 << 20), cabi.RK_ERR_WORKSPACE,
          "256-byte aligned"),
         # Schedule bits: both at once, or an unknown bit, are invalid; the queue needs the MFMA variant,
-        # a split-K shape (several partitions), at most 256 partitions and at most 1024 sequences.
+        # a split-K shape (several partitions), at most 256 partitions and at most 64512 sequences
+        # (launches of 1024).
         (dict(variant=0x300), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
         (dict(variant=0x800), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
         (dict(variant=0x700), cabi.RK_ERR_INVALID_ARGUMENT, "variant"),
@@ -153,7 +154,7 @@ def call(lib, **overrides):
         (dict(variant=0x200), cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
         (dict(variant=0x200, max_blocks=1024, partition_tokens=16, workspace=1 << 20, workspace_bytes=1 << 30),
          cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
-        (dict(variant=0x200, batch=1025, max_blocks=64, workspace=1 << 20, workspace_bytes=1 << 30),
+        (dict(variant=0x200, batch=64513, max_blocks=64, workspace=1 << 20, workspace_bytes=1 << 40),
          cabi.RK_ERR_UNSUPPORTED, "work-queue schedule"),
     ],
 )

@@ -203,8 +203,9 @@ def test_phase_entry_points_validate_identically(lib):
 
 
 def test_counter_words_formula(lib):
-    """One arrival counter per (sequence, KV head, head chunk), chunks of 1, 2 or 4 query heads, then the
-    work queue's ticket and exit counters."""
+    """One arrival counter per (sequence, KV head, chunk of 1, 2 or 4 query heads) -- an upper bound for
+    the 8-head chunks groups of 8 or more run at head_dim <= 128 -- then the work queue's ticket and
+    exit counters."""
 
     for batch, hq, hkv, arrivals in [(128, 32, 8, 128 * 8), (3, 64, 8, 3 * 8 * 2), (2, 12, 4, 2 * 4),
                                      (5, 8, 8, 40), (1, 16, 8, 8), (2, 40, 8, 2 * 8 * 2)]:

@@ -91,7 +91,8 @@ SHAPES = [
     (8, 8, 64, 16, "fp16"),
     (16, 8, 64, 32, "bf16"),
     (12, 4, 128, 16, "bf16"),   # group 3: one padded head slot
-    (64, 8, 128, 16, "fp16"),   # group 8: two head chunks, the first one stores
+    (64, 8, 128, 16, "fp16"),   # group 8: one 8-head chunk, which stores
+    (128, 8, 64, 16, "bf16"),   # group 16: two 8-head chunks, the first one stores
     (32, 8, 256, 16, "bf16"),
     (4, 4, 256, 8, "fp16"),     # blocks smaller than a tile
     (8, 2, 128, 1, "fp16"),     # one token per block

@@ -40,13 +40,14 @@ def ragged_contexts(batch, limit, seed):
 
 
 # (query_heads, kv_heads, head_dim, block_size, dtype, index_dtype, partition): head chunks of 4, 1,
-# 2 and two chunks of 4; blocks of 16, 32, 8 and 1 tokens; every head_dim.
+# 2 and 8 and two chunks of 4 (group 8 at head_dim 256); blocks of 16, 32, 8 and 1 tokens; every head_dim.
 SHAPES = [
     (32, 8, 128, 16, "bf16", "int32", 128),
     (16, 16, 64, 32, "bf16", "int64", 64),
     (16, 8, 128, 8, "fp16", "int64", 128),
     (64, 8, 128, 1, "bf16", "int32", 64),
     (32, 8, 256, 16, "fp16", "int32", 128),
+    (64, 8, 256, 16, "bf16", "int32", 256),
 ]
 
 

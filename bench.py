@@ -11,22 +11,27 @@ one-thread kernel that zeroes its ticket counter), else one workgroup per work i
 128, block 16, bf16, context lengths ~ U[1024, 16384] (seeded), about 4.8 GB of K/V per call -- 18x
 the 256 MB last-level cache, so every call streams from HBM.
 
+Timing: every form below is timed as S (--samples, default 10) interleaved samples of K (--steps)
+back-to-back launches, each sample bracketed by synchronisations and HIP events on the launch
+stream; consecutive samples run the forms in opposite orders.  Reported figures are medians over
+the samples; timing.cv_pct_events is the headline form's coefficient of variation.
+
 Prints one JSON line:
   value            effective KV GB/s = algorithmic K+V bytes per call / wall time per call
-  us_per_call      wall time per call over the timed region: K whole calls back to back, nothing
-                   else on the stream (us_per_call_events: the same region by HIP events)
+  us_per_call      median wall time per call of the headline form: K whole calls back to back,
+                   nothing else on the stream (us_per_call_events: the same samples by HIP events)
   roofline         the partition kernel against the 8 TB/s HBM peak: achieved = KV bytes / its
-                   average duration, from HIP events recorded on the launch stream around K
-                   back-to-back launches of that kernel alone (in the fused form the call is that
-                   one kernel, plus the queue's counter reset on the work-queue schedule); traffic = measured HBM bytes per launch from the committed
-                   rocprofv3 counter summary for this exact configuration (null when there is none)
+                   median duration by HIP events (in the fused form the call is that one kernel,
+                   plus the queue's counter reset on the work-queue schedule); traffic = measured
+                   HBM bytes per launch from the committed rocprofv3 counter summary for this exact
+                   configuration (null when there is none)
   kernels_us       per-launch averages of the reduce form's two kernels; us_per_call_reduce and
                    us_per_call_fused time both whole-call forms (omitted with --no-breakdown, which
                    times the headline form only)
   cpu_baseline     the reference algorithm (its torch fallback, restated in oracle/) on the host
                    cores over a bounded sample of the same workload
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5] [--variant mfma]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--samples S] [--workload c5] [--variant mfma]
                        [--partition P] [--merge fused|reduce] [--schedule auto|grid|queue]
                        [--no-breakdown] [--no-cpu-baseline]
                        [--cpu-seconds S] [--calibration-copy]
@@ -42,6 +47,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -63,10 +69,12 @@ def parse_args(argv=None):
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--samples", type=int, default=10,
+                        help="interleaved samples of --steps calls per timed form (medians reported)")
     parser.add_argument("--workload", default="c5",
                         help="c1..c5 (the five measured shapes) or one of the reference's decode cases, "
                              "<case id>-<fp16|bf16> (benchmarks/workloads/paged_attention_decode-1.0.yaml)")
-    parser.add_argument("--variant", default=None, choices=["mfma", "valu"])
+    parser.add_argument("--variant", default=None, choices=["mfma", "valu", "mfma_qk"])
     parser.add_argument("--partition", type=int, default=None)
     parser.add_argument("--merge", default=None, choices=["fused", "reduce"],
                         help="partition-record merge form (default: the workload's dispatch entry)")
@@ -647,7 +655,6 @@ def main(argv=None) -> int:
         Returns (average µs per launch by the events, wall µs per launch by the host clock)."""
 
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        prepare(phase)  # outside the timed region
         torch.cuda.synchronize()
         t = time.perf_counter()
         start.record(stream)
@@ -658,20 +665,41 @@ def main(argv=None) -> int:
         wall = time.perf_counter() - t
         return start.elapsed_time(end) * 1e3 / args.steps, wall * 1e6 / args.steps
 
-    # The contract's timed region: K whole decode calls, nothing else on the stream.  In the fused
-    # form that is K launches of the partition kernel (its average duration is the roofline
-    # figure).  The breakdown times each kernel of the reduce form on its own, K launches each
-    # (the reduce form's roofline figure is its partition kernel), and the other whole-call form.
-    event_us, us_per_call = region(headline)
-    part_avg = red_avg = None
-    forms = {merge: us_per_call}
+    # The timed regions.  Every form bench reports is timed as S interleaved samples of K launches
+    # (the reference's protocol: paired, order-alternating samples, benchmark.py:221-229 with the
+    # workload file's 30 samples and 3% CV gate, benchmarks/workloads/paged_attention_decode-1.0.yaml:8-11):
+    # sample s runs the headline form (K whole decode calls, nothing else on the stream), then the
+    # reduce form's partition kernel and merge kernel alone, then the other whole-call form, and
+    # sample s + 1 runs them in the reverse order, so no form always runs first.  value, ms_per_step
+    # and roofline.frac are medians over the headline samples.  In the fused form the call is the
+    # partition kernel alone (its average duration is the roofline figure); the reduce form's
+    # roofline figure is its partition kernel.
+    phases = [headline]
     if not args.no_breakdown or merge == "reduce":
-        part_avg, _ = region("partitions")
-        # One partition covering every sequence needs no reduce launch (the call launches one kernel).
-        red_avg = region("reduce")[0] if need > 0 else None
+        phases.append("partitions")
+        if need > 0:  # one partition covering every sequence needs no reduce launch
+            phases.append("reduce")
+    other = "reduce" if merge == "fused" else "fused"
     if not args.no_breakdown:
-        other = "reduce" if merge == "fused" else "fused"
-        forms[other] = region("fused" if other == "fused" else "all")[1]
+        phases.append("fused" if other == "fused" else "all")
+    for phase in phases:
+        prepare(phase)  # outside the timed regions
+    samples = {phase: [] for phase in phases}
+    for s_index in range(args.samples):
+        for phase in (phases if s_index % 2 == 0 else phases[::-1]):
+            samples[phase].append(region(phase))
+
+    def median_of(phase: str, which: int) -> float:
+        return statistics.median(x[which] for x in samples[phase])
+
+    event_us, us_per_call = median_of(headline, 0), median_of(headline, 1)
+    head_events = [x[0] for x in samples[headline]]
+    cv_pct = statistics.pstdev(head_events) / statistics.mean(head_events) * 100
+    part_avg = median_of("partitions", 0) if "partitions" in samples else None
+    red_avg = median_of("reduce", 0) if "reduce" in samples else None
+    forms = {merge: us_per_call}
+    if not args.no_breakdown:
+        forms[other] = median_of("fused" if other == "fused" else "all", 1)
     kernel_avg = part_avg if merge == "reduce" else event_us
     gbps = kv_bytes / (us_per_call * 1e3)
     achieved = kv_bytes / (kernel_avg * 1e3)
@@ -698,8 +726,8 @@ def main(argv=None) -> int:
         # rewrite one slot per sequence of each copy; the decode timings above are already taken).
         from radeon_kernels.cabi import kv_library
 
-        if variant != "mfma":
-            raise SystemExit("--append needs the mfma variant")
+        if variant not in ("mfma", "mfma_qk"):
+            raise SystemExit("--append needs an mfma variant")
         kvlib = kv_library()
         gen = torch.Generator(device=device).manual_seed(data["seed"] + 1)
         new_k = torch.randn((batch, hkv, d), generator=gen, device=device).to(q.dtype)
@@ -762,6 +790,9 @@ def main(argv=None) -> int:
         },
         "us_per_call": round(us_per_call, 2),
         "us_per_call_events": round(event_us, 2),
+        "timing": {"samples": args.samples, "calls_per_sample": args.steps, "statistic": "median",
+                   "interleaved_forms": phases, "cv_pct_events": round(cv_pct, 3),
+                   "us_per_call_events_samples": [round(x, 2) for x in head_events]},
         "pct_hbm_peak": round(gbps / HBM_PEAK_GBPS * 100, 2),
         "kv_bytes_per_call": kv_bytes,
         "kernels_us": None if part_avg is None else {

@@ -68,9 +68,12 @@ extern "C" {
 #define RK_INDEX_INT32 0
 #define RK_INDEX_INT64 1
 
-/* Kernel variants: how QK^T is computed (PV always runs on the vector ALUs). */
-#define RK_PA_VARIANT_MFMA 0 /* v_mfma_f32_16x16x32_{bf16,f16}, one 16-token tile per wave step */
-#define RK_PA_VARIANT_VALU 1 /* fp32 FMAs + DPP row reductions */
+/* Kernel variants: where QK^T and PV are computed.  All three give results within the operator's
+ * tolerances.  PV on MFMA takes each fp32 probability as a rounded high part plus its residual
+ * (about 2^-16 relative), so its products match the fp32 FMAs' to within fp32 accumulation. */
+#define RK_PA_VARIANT_MFMA 0    /* QK^T and PV on v_mfma_f32_16x16x32_{bf16,f16} */
+#define RK_PA_VARIANT_VALU 1    /* QK^T on fp32 FMAs + DPP row reductions, PV on fp32 FMAs */
+#define RK_PA_VARIANT_MFMA_QK 2 /* QK^T on MFMA, PV on fp32 FMAs */
 
 /*
  * Schedule of the partition kernel, OR-ed into the variant argument (no reference counterpart).
@@ -84,7 +87,7 @@ extern "C" {
  *                         hold tokens from a ticket counter: in the workspace header, zeroed by a
  *                         one-thread kernel launched first, or, for rk_pa_decode_fused and the fused
  *                         rk_pa_decode_append, in the last two words of the counter array, which the
- *                         launch's last workgroup leaves zero (one launch).  Eligible: RK_PA_VARIANT_MFMA, a split-K shape
+ *                         launch's last workgroup leaves zero (one launch).  Eligible: RK_PA_VARIANT_MFMA or _MFMA_QK, a split-K shape
  *                         (rk_pa_decode_workspace_bytes > 0) with at most 256 partitions per
  *                         sequence and at most 64512 sequences; RK_ERR_UNSUPPORTED otherwise.
  * A batch of more than 1024 sequences on an eligible call runs as consecutive launches of 1024
@@ -139,7 +142,7 @@ int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t hea
  *
  * partition_tokens: context tokens per workgroup (split-K partition); a multiple of 16 in
  *   [16, 8192] with partition_tokens / block_size <= 256.
- * variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_VALU, optionally OR-ed with one RK_PA_SCHEDULE_* bit
+ * variant: RK_PA_VARIANT_MFMA, RK_PA_VARIANT_VALU or RK_PA_VARIANT_MFMA_QK, optionally OR-ed with one RK_PA_SCHEDULE_* bit
  *   and with RK_PA_PARTITION_GROW.
  * workspace/workspace_bytes: device buffer of at least rk_pa_decode_workspace_bytes(...) bytes
  *   (may be NULL/0 when that is zero).  Its contents need no initialisation.
@@ -222,7 +225,7 @@ int rk_pa_decode_fused(const void* query, const void* key_cache, const void* val
  *
  * counters/counter_words: NULL for the two-launch form (partition kernel, then the reduce kernel
  * when a sequence can span several partitions), or the counters of rk_pa_decode_fused for the
- * single-launch form.  variant: RK_PA_VARIANT_MFMA only (RK_ERR_UNSUPPORTED otherwise).
+ * single-launch form.  variant: RK_PA_VARIANT_MFMA or RK_PA_VARIANT_MFMA_QK (RK_ERR_UNSUPPORTED otherwise).
  */
 int rk_pa_decode_append(const void* query, const void* new_key, const void* new_value, void* key_cache,
                         void* value_cache, const void* block_tables, const void* context_lengths,

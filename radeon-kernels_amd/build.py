@@ -125,15 +125,30 @@ class Library:
     all built from the same binding source."""
 
     def __init__(self, hip_source: str, cabi_name: str, binding_source: str,
-                 bindings: dict[str, tuple[str, ...]]) -> None:
+                 bindings: dict[str, tuple[str, ...]], units: tuple[tuple[str, tuple[str, ...]], ...] = ()) -> None:
         self.hip_source = CSRC / hip_source
         self.cabi_name = cabi_name
         self.binding_source = CSRC / binding_source
         self.bindings = bindings
+        # Further HIP compilations linked into the same library: (source, preprocessor definitions).
+        self.units = tuple((CSRC / source, defines) for source, defines in units)
+
+    def hip_compilations(self) -> list[tuple[Path, tuple[str, ...], str]]:
+        """(source, definitions, object stem) of every HIP compilation of this library."""
+
+        out = [(self.hip_source, (), self.hip_source.stem)]
+        for source, defines in self.units:
+            suffix = "_".join(d.split("=", 1)[1] for d in defines)
+            out.append((source, defines, f"{source.stem}_{suffix}"))
+        return out
 
 
 LIBRARIES = (
-    Library("pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", {EXTENSION_NAME: ("paged_attention_decode",)}),
+    # The decode kernels compile once per (element type, head_dim), concurrently: one compilation of
+    # every instantiation took about 7 minutes, a unit takes about one.
+    Library("pa_decode_gfx950.hip", CABI_NAME, "pa_torch_ext.cpp", {EXTENSION_NAME: ("paged_attention_decode",)},
+            units=tuple(("pa_decode_kernels.hip", (f"RK_PA_UNIT_ELEMENT={element}", f"RK_PA_UNIT_HEAD_DIM={head_dim}"))
+                        for element in ("bf16", "fp16") for head_dim in (64, 128, 256))),
     Library("kv_cache_gfx950.hip", "librk_kv_gfx950.so", "kv_torch_ext.cpp",
             {"rk_kv_append_gfx950": ("kv_cache_append",), "rk_kv_copy_gfx950": ("kv_cache_copy",)}),
     Library("sdpa_gfx950.hip", "librk_sdpa_gfx950.so", "sdpa_torch_ext.cpp", {"rk_sdpa_gfx950": ("sdpa",)}),
@@ -157,9 +172,11 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
     # object exists.
     jobs = []
     for lib in LIBRARIES:
-        kernel_obj = work / f"{lib.hip_source.stem}.o"
-        hip = _run([_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(lib.hip_source), "-o", str(kernel_obj)],
-                   verbose)
+        hip = []
+        for source, defines, stem in lib.hip_compilations():
+            obj = work / f"{stem}.o"
+            hip.append((obj, _run([_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *[f"-D{d}" for d in defines], "-c",
+                                   str(source), "-o", str(obj)], verbose)))
         objects = {}
         for module in lib.bindings:
             ext_obj = work / f"{module}.o"
@@ -183,14 +200,16 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
                 str(ext_obj),
             ]
             objects[module] = (ext_obj, _run(cxx, verbose))
-        jobs.append((lib, kernel_obj, hip, objects))
+        jobs.append((lib, hip, objects))
 
     rocm_lib = str(Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib")
     bindings: dict[str, Path] = {}
-    for lib, kernel_obj, hip, objects in jobs:
-        _finish(hip, f"hipcc ({lib.hip_source.name})")
+    for lib, hip, objects in jobs:
+        for obj, process in hip:
+            _finish(process, f"hipcc ({obj.stem})")
+        kernel_objs = [str(obj) for obj, _ in hip]
         cabi_tmp = work / lib.cabi_name
-        _finish(_run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(kernel_obj), "-Wl,--build-id=none",
+        _finish(_run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *kernel_objs, "-Wl,--build-id=none",
                       "-o", str(cabi_tmp)], verbose), f"hipcc link ({lib.cabi_name})")
         linked = []
         for module, (ext_obj, gxx) in objects.items():
@@ -200,7 +219,7 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
                 "g++",
                 "-shared",
                 str(ext_obj),
-                str(kernel_obj),
+                *kernel_objs,
                 *[f"-L{path}" for path in libraries],
                 f"-L{rocm_lib}",
                 "-lamdhip64",
@@ -222,7 +241,8 @@ def compile_libraries(verbose: bool = False) -> dict[str, Path]:
             ext_obj.unlink()
             for operator in lib.bindings[module]:
                 bindings[operator] = LIB_DIR / f"{module}.so"
-        kernel_obj.unlink()
+        for obj, _ in hip:
+            obj.unlink()
     return bindings
 
 
@@ -273,23 +293,8 @@ def compile_launch_loops(verbose: bool = False) -> Path:
     return target
 
 
-def compile_read_probe(verbose: bool = False) -> Path:
-    """The read-only HBM probe program (benchmarks/read_probe.hip): no library, no torch."""
-
-    source = PACKAGE_ROOT / "benchmarks" / "read_probe.hip"
-    target = PACKAGE_ROOT / "benchmarks" / "read_probe"
-    temporary = PACKAGE_ROOT / "_build" / "read_probe"
-    temporary.parent.mkdir(exist_ok=True)
-    flags = [flag for flag in HIPCC_FLAGS if flag != "-fPIC"]
-    _finish(_run([_hipcc(), *flags, str(source), "-Wl,--build-id=none", "-o", str(temporary)], verbose),
-            "hipcc (read_probe.hip)")
-    os.replace(temporary, target)
-    return target
-
-
 def build(verbose: bool = False) -> dict:
     compile_launch_loops(verbose)
-    compile_read_probe(verbose)
     summary = write_pack_and_dispatch(compile_libraries(verbose=verbose))
     # Sign the pack manifest (the runtime loads only signed packs) and rewrite the promotion records
     # from the committed GPU evaluations (promotion/publish.py).

@@ -219,6 +219,14 @@ at::Tensor decode_valu(const at::Tensor& query, const at::Tensor& key_cache,
                 partition_tokens, merge, RK_PA_VARIANT_VALU | grow_bits(grow_partitions));
 }
 
+at::Tensor decode_mfma_qk(const at::Tensor& query, const at::Tensor& key_cache,
+                          const at::Tensor& value_cache, const at::Tensor& block_tables,
+                          const at::Tensor& context_lengths, double scale, int64_t partition_tokens,
+                          const std::string& merge, bool grow_partitions) {
+  return decode(query, key_cache, value_cache, block_tables, context_lengths, scale,
+                partition_tokens, merge, RK_PA_VARIANT_MFMA_QK | grow_bits(grow_partitions));
+}
+
 // Append-and-decode: writes each sequence's new token into the caches (in place) and returns the
 // decode of the updated context, as kv_cache_append followed by decode_mfma would.
 at::Tensor decode_append_mfma(const at::Tensor& query, const at::Tensor& new_key,
@@ -233,8 +241,8 @@ at::Tensor decode_append_mfma(const at::Tensor& query, const at::Tensor& new_key
 }  // namespace
 
 PYBIND11_MODULE(rk_pa_gfx950, module) {
-  module.doc() = "gfx950 split-K paged-attention decode (MFMA QK^T or VALU QK^T, VALU PV)";
-  module.def("decode_mfma", &decode_mfma, "paged decode, QK^T on MFMA", py::arg("query"),
+  module.doc() = "gfx950 split-K paged-attention decode (QK^T and PV on MFMA or on fp32 FMAs)";
+  module.def("decode_mfma", &decode_mfma, "paged decode, QK^T and PV on MFMA", py::arg("query"),
              py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
              py::arg("context_lengths"), py::arg("scale"), py::kw_only(),
              py::arg("partition_tokens") = 512, py::arg("merge") = "auto",
@@ -244,6 +252,11 @@ PYBIND11_MODULE(rk_pa_gfx950, module) {
              py::arg("query"), py::arg("new_key"), py::arg("new_value"), py::arg("key_cache"),
              py::arg("value_cache"), py::arg("block_tables"), py::arg("context_lengths"), py::arg("scale"),
              py::kw_only(), py::arg("partition_tokens") = 512, py::arg("merge") = "auto",
+             py::arg("grow_partitions") = false);
+  module.def("decode_mfma_qk", &decode_mfma_qk, "paged decode, QK^T on MFMA, PV on fp32 FMAs", py::arg("query"),
+             py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),
+             py::arg("context_lengths"), py::arg("scale"), py::kw_only(),
+             py::arg("partition_tokens") = 512, py::arg("merge") = "auto",
              py::arg("grow_partitions") = false);
   module.def("decode_valu", &decode_valu, "paged decode, QK^T on fp32 FMAs", py::arg("query"),
              py::arg("key_cache"), py::arg("value_cache"), py::arg("block_tables"),

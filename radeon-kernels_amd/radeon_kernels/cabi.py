@@ -29,7 +29,7 @@ RK_DTYPE_BF16 = 1
 RK_INDEX_INT32 = 0
 RK_INDEX_INT64 = 1
 RK_PA_NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
-VARIANTS = {"mfma": 0, "valu": 1}
+VARIANTS = {"mfma": 0, "valu": 1, "mfma_qk": 2}
 # Partition-kernel schedule bits OR-ed into the variant (RK_PA_SCHEDULE_*); "auto" lets the library
 # choose.
 SCHEDULES = {"auto": 0, "grid": 0x100, "queue": 0x200}

@@ -70,7 +70,8 @@ def test_status_codes_match_header():
         value = int(re.search(rf"#define {name} (\d+)", text).group(1))
         assert getattr(cabi, name) == value, name
     assert cabi.VARIANTS == {"mfma": int(re.search(r"RK_PA_VARIANT_MFMA (\d+)", text).group(1)),
-                             "valu": int(re.search(r"RK_PA_VARIANT_VALU (\d+)", text).group(1))}
+                             "valu": int(re.search(r"RK_PA_VARIANT_VALU (\d+)", text).group(1)),
+                             "mfma_qk": int(re.search(r"RK_PA_VARIANT_MFMA_QK (\d+)", text).group(1))}
     assert cabi.SCHEDULES == {"auto": 0, "grid": int(re.search(r"RK_PA_SCHEDULE_GRID (0x[0-9a-f]+)", text).group(1), 16),
                               "queue": int(re.search(r"RK_PA_SCHEDULE_QUEUE (0x[0-9a-f]+)", text).group(1), 16)}
     assert cabi.RK_PA_PARTITION_GROW == int(re.search(r"RK_PA_PARTITION_GROW (0x[0-9a-f]+)", text).group(1), 16)

@@ -94,19 +94,34 @@ def test_each_launch_grows_on_its_own(gpu, palib, big):
         assert _same(fixed[lo:hi], grown[lo:hi]), f"launch {launch} at {sizes[launch]} tokens"
 
 
-def test_append_and_decode_over_1024_sequences(gpu, palib, big):
+def test_append_and_decode_over_1024_sequences(gpu, palib, kvlib, big):
+    """Grid and fused work-queue append-and-decode, each on its own fresh copy of the caches: equal
+    outputs, and caches equal to what kv_cache_append of the same rows writes into a third copy."""
+
     import torch
 
     _, d = big
     gen = torch.Generator(device=gpu).manual_seed(3)
     new_k = torch.randn(BATCH, 2, 128, generator=gen, device=gpu).to(torch.float16)
     new_v = torch.randn(BATCH, 2, 128, generator=gen, device=gpu).to(torch.float16)
-    k, v = d["key_cache"].clone(), d["value_cache"].clone()
-    args = (d["query"], k, v, d["block_tables"], d["context_lengths"])
+    bt, cl = d["block_tables"], d["context_lengths"]
     announce("1030 sequences: append-and-decode")
-    grid = palib.decode(*args, partition_tokens=256, new_key=new_k, new_value=new_v, schedule="grid")
-    k_grid, v_grid = k.clone(), v.clone()
-    queue = palib.decode(*args, partition_tokens=256, new_key=new_k, new_value=new_v, phase="fused")
+    caches = {}
+    outs = {}
+    for form, extra in (("grid", dict(schedule="grid")), ("queue", dict(phase="fused"))):
+        k, v = d["key_cache"].clone(), d["value_cache"].clone()
+        outs[form] = palib.decode(d["query"], k, v, bt, cl, partition_tokens=256, new_key=new_k, new_value=new_v,
+                                  **extra)
+        caches[form] = (k, v)
+    # The same rows through kv_cache_append: slot of position context_length - 1 (every context here
+    # lies inside the table).
+    bs = d["key_cache"].shape[1]
+    pos = cl.long() - 1
+    slots = bt.long().gather(1, (pos // bs).unsqueeze(1)).squeeze(1) * bs + pos % bs
+    k_ref, v_ref = d["key_cache"].clone(), d["value_cache"].clone()
+    kvlib.append(new_k, new_v, k_ref, v_ref, slots)
     torch.cuda.synchronize()
-    assert _same(queue, grid)
-    assert torch.equal(k, k_grid) and torch.equal(v, v_grid)
+    assert _same(outs["queue"], outs["grid"])
+    assert not torch.equal(k_ref, d["key_cache"])  # the appends wrote something
+    for form, (k, v) in caches.items():
+        assert torch.equal(k, k_ref) and torch.equal(v, v_ref), f"{form} form's caches differ from kv_cache_append"

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 WORKLOAD_PARTITIONS = {"c1": 128, "c2": 64, "c3": 128, "c4": 64, "c5": 2048}
 
 
-@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("variant", ["mfma", "valu", "mfma_qk"])
 @pytest.mark.parametrize("key", ["c1", "c2", "c3", "c4"])
 def test_measured_workloads_match_oracle(gpu, palib, key, variant):
     import torch
@@ -40,7 +40,7 @@ def test_measured_workloads_match_oracle(gpu, palib, key, variant):
     assert_within(out, fp32.numpy().astype(np.float64), w.dtype, f"{key}/{variant} vs fp32 fallback")
 
 
-@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("variant", ["mfma", "valu", "mfma_qk"])
 def test_ragged_b128_workload(gpu, palib, c5_case, variant):
     """All 128 sequences of the headline workload against the float64 oracle."""
 
@@ -56,7 +56,7 @@ def test_ragged_b128_workload(gpu, palib, c5_case, variant):
 
 
 @pytest.mark.parametrize("partition", [16, 64, 256, 1024, 4096])
-@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("variant", ["mfma", "valu", "mfma_qk"])
 def test_partition_sizes_agree(gpu, palib, partition, variant):
     case = make_case(__import__("torch"), batch=4, query_heads=32, kv_heads=8, head_dim=128, block_size=16,
                      contexts=[1, 17, 1000, 3333], dtype="bf16", seed=11)
@@ -84,7 +84,7 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("variant", ["mfma", "valu", "mfma_qk"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_shape_sweep(gpu, palib, shape, variant):
     import torch
@@ -99,7 +99,8 @@ def test_shape_sweep(gpu, palib, shape, variant):
     assert_within(out, oracle64(case), dtype, f"shape {shape}")
 
 
-def test_context_edges(gpu, palib):
+@pytest.mark.parametrize("variant", ["mfma", "mfma_qk"])
+def test_context_edges(gpu, palib, variant):
     """ctx=1 (output is that V row), block boundaries, full table, over-long and empty contexts."""
 
     import torch
@@ -109,10 +110,10 @@ def test_context_edges(gpu, palib):
     case = make_case(torch, batch=len(contexts), query_heads=8, kv_heads=2, head_dim=128, block_size=bs,
                      contexts=contexts, max_blocks=mb, dtype="fp16", seed=5)
     dev = to_device(case, gpu)
-    announce("context edges")
+    announce(f"context edges variant={variant}")
     for partition in (16, 64, 4096):
         out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
-                           dev["context_lengths"], partition_tokens=partition).cpu()
+                           dev["context_lengths"], partition_tokens=partition, variant=variant).cpu()
         assert_within(out, oracle64(case), "fp16", f"edges partition {partition}")
         assert torch.isnan(out[5]).all() and torch.isnan(out[6]).all()
         # ctx = 1: softmax weight 1 on token 0, so the output is exactly token 0's V row.
@@ -133,7 +134,8 @@ def test_int64_indices_and_explicit_scale(gpu, palib):
     assert_within(out, oracle64(case, scale=0.05), "bf16", "int64/explicit scale")
 
 
-def test_out_of_range_block_ids_are_skipped(gpu, palib):
+@pytest.mark.parametrize("variant", ["mfma", "mfma_qk"])
+def test_out_of_range_block_ids_are_skipped(gpu, palib, variant):
     import torch
 
     case = make_case(torch, batch=1, query_heads=8, kv_heads=2, head_dim=64, block_size=16,
@@ -143,9 +145,9 @@ def test_out_of_range_block_ids_are_skipped(gpu, palib):
     bad[0, 1] = num_blocks + 1000   # tokens 16..31 point outside the cache
     bad[0, 2] = -1                  # tokens 32..47 likewise
     dev = to_device(case, gpu)
-    announce("out-of-range block ids")
+    announce(f"out-of-range block ids variant={variant}")
     out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], bad.to(gpu),
-                       dev["context_lengths"], partition_tokens=16)
+                       dev["context_lengths"], partition_tokens=16, variant=variant)
     # Same as attending only over the valid tokens: blocks 0 and 3 (tokens 0-15, 48-63).
     keep = case["block_tables"][0, [0, 3]]
     compact = dict(case)
@@ -154,7 +156,8 @@ def test_out_of_range_block_ids_are_skipped(gpu, palib):
     assert_within(out, oracle64(compact), "fp16", "skipped blocks")
 
 
-def test_non_finite_propagates(gpu, palib):
+@pytest.mark.parametrize("variant", ["mfma", "mfma_qk"])
+def test_non_finite_propagates(gpu, palib, variant):
     import torch
 
     case = make_case(torch, batch=2, query_heads=8, kv_heads=2, head_dim=128, block_size=16,
@@ -162,21 +165,22 @@ def test_non_finite_propagates(gpu, palib):
     block = int(case["block_tables"][0, 1])
     case["key_cache"][block, 3, 1, 7] = float("nan")  # sequence 0, token 19, KV head 1
     dev = to_device(case, gpu)
-    announce("NaN in K")
+    announce(f"NaN in K variant={variant}")
     out = palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"],
-                       dev["context_lengths"], partition_tokens=16).cpu()
+                       dev["context_lengths"], partition_tokens=16, variant=variant).cpu()
     assert torch.isnan(out[0, 4:8]).all()          # query heads of KV head 1
     assert torch.isfinite(out[0, 0:4]).all() and torch.isfinite(out[1]).all()
 
 
-def test_deterministic(gpu, palib):
+@pytest.mark.parametrize("variant", ["mfma", "mfma_qk"])
+def test_deterministic(gpu, palib, variant):
     import torch
     from benchmarks.workloads import make_inputs
 
     data = to_device(make_inputs("c2"), gpu)
-    announce("determinism c2")
+    announce(f"determinism c2 variant={variant}")
     runs = [palib.decode(data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
-                         data["context_lengths"], partition_tokens=64) for _ in range(3)]
+                         data["context_lengths"], partition_tokens=64, variant=variant) for _ in range(3)]
     assert all(torch.equal(runs[0], r) for r in runs[1:])
 
 
@@ -196,7 +200,7 @@ def _fused_vs_two_launch(palib, dev, partition, counters, variant="mfma"):
     return fused
 
 
-@pytest.mark.parametrize("variant", ["mfma", "valu"])
+@pytest.mark.parametrize("variant", ["mfma", "valu", "mfma_qk"])
 @pytest.mark.parametrize("key", ["c1", "c2", "c3", "c4"])
 def test_fused_matches_two_launch_on_measured_workloads(gpu, palib, key, variant):
     import torch
@@ -210,9 +214,10 @@ def test_fused_matches_two_launch_on_measured_workloads(gpu, palib, key, variant
     assert_within(out, oracle64(data), data["workload"].dtype, f"fused {key}/{variant} vs float64 oracle")
 
 
+@pytest.mark.parametrize("variant", ["mfma", "mfma_qk"])
 @pytest.mark.parametrize("partition", [16, 64, 1024])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_fused_shape_sweep(gpu, palib, shape, partition):
+def test_fused_shape_sweep(gpu, palib, shape, partition, variant):
     import torch
 
     hq, hkv, d, bs, dtype = shape
@@ -221,9 +226,9 @@ def test_fused_shape_sweep(gpu, palib, shape, partition):
     case = make_case(torch, batch=3, query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bs,
                      contexts=[5, bs * 3 + 1, 1500], dtype=dtype, seed=hq * 5 + d + bs)
     dev = to_device(case, gpu)
-    announce(f"fused shape {shape} partition={partition}")
+    announce(f"fused shape {shape} partition={partition} variant={variant}")
     counters = torch.zeros(palib.counter_words(3, hq, hkv), dtype=torch.int32, device=gpu)
-    out = _fused_vs_two_launch(palib, dev, partition, counters)
+    out = _fused_vs_two_launch(palib, dev, partition, counters, variant)
     assert_within(out, oracle64(case), dtype, f"fused shape {shape}")
 
 
@@ -250,12 +255,13 @@ def test_fused_counters_serve_consecutive_calls_of_different_shapes(gpu, palib):
             assert_within(out, oracle64(case), case["dtype"], f"consecutive case {i}")
 
 
-def test_fused_ragged_b128_matches_two_launch(gpu, palib, c5_case):
+@pytest.mark.parametrize("variant", ["mfma", "mfma_qk"])
+def test_fused_ragged_b128_matches_two_launch(gpu, palib, c5_case, variant):
     import torch
 
-    announce("fused c5 ragged b128")
+    announce(f"fused c5 ragged b128 variant={variant}")
     data = c5_case["gpu"]
     counters = torch.zeros(palib.counter_words(128, 32, 8), dtype=torch.int32, device=gpu)
     for _ in range(2):
-        out = _fused_vs_two_launch(palib, data, 2048, counters)
+        out = _fused_vs_two_launch(palib, data, 2048, counters, variant)
     assert_within(out, c5_case["expected"], "bf16", "fused c5 all 128 rows")

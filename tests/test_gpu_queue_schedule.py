@@ -56,8 +56,9 @@ def shape_id(shape):
     return f"h{hq}x{hkv}-d{d}-bs{bs}-{dtype}-{index}-p{partition}"
 
 
+@pytest.mark.parametrize("variant", ["mfma", "mfma_qk"])
 @pytest.mark.parametrize("shape", SHAPES, ids=shape_id)
-def test_queue_matches_grid_and_oracle(gpu, palib, shape):
+def test_queue_matches_grid_and_oracle(gpu, palib, shape, variant):
     import torch
 
     hq, hkv, d, bs, dtype, index, partition = shape
@@ -68,10 +69,10 @@ def test_queue_matches_grid_and_oracle(gpu, palib, shape):
                      contexts=contexts, max_blocks=max_blocks, dtype=dtype, index_dtype=index, seed=11)
     dev = to_device(case, gpu)
     args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
-    announce(f"queue vs grid {shape_id(shape)} batch {batch}")
-    grid = palib.decode(*args, partition_tokens=partition, schedule="grid")
-    queue = palib.decode(*args, partition_tokens=partition, schedule="queue")
-    auto = palib.decode(*args, partition_tokens=partition)
+    announce(f"queue vs grid {shape_id(shape)} batch {batch} variant={variant}")
+    grid = palib.decode(*args, partition_tokens=partition, schedule="grid", variant=variant)
+    queue = palib.decode(*args, partition_tokens=partition, schedule="queue", variant=variant)
+    auto = palib.decode(*args, partition_tokens=partition, variant=variant)
     torch.cuda.synchronize()
     assert same_bits(queue, grid)
     assert same_bits(auto, grid)
@@ -188,11 +189,12 @@ def test_ragged_b128_workload_schedules_agree(gpu, palib, c5_case):
 
     dev = c5_case["gpu"]
     args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
-    announce("queue b128 ragged P=2048")
-    grid = palib.decode(*args, partition_tokens=2048, schedule="grid")
-    auto = palib.decode(*args, partition_tokens=2048)
-    torch.cuda.synchronize()
-    assert same_bits(auto, grid)
+    for variant in ("mfma", "mfma_qk"):
+        announce(f"queue b128 ragged P=2048 variant={variant}")
+        grid = palib.decode(*args, partition_tokens=2048, schedule="grid", variant=variant)
+        auto = palib.decode(*args, partition_tokens=2048, variant=variant)
+        torch.cuda.synchronize()
+        assert same_bits(auto, grid)
 
 
 def test_schedule_query_names_what_runs(gpu, palib):

@@ -95,22 +95,3 @@ def test_noalloc_allocates_nothing_after_setup(gpu, palib):
     assert torch.cuda.memory_stats()["allocation.all.allocated"] == allocated_before
     for out in outs[1:]:
         assert torch.equal(out.view(torch.int16), outs[0].view(torch.int16))
-
-
-def test_noalloc_rejects_shapes_beyond_its_scratch(gpu, palib):
-    """A shape needing more records than the scratch array holds fails before any launch."""
-
-    import torch
-
-    case = make_case(torch, batch=2, query_heads=8, kv_heads=2, head_dim=128, block_size=16,
-                     contexts=[40, 40], dtype="bf16", seed=33)
-    dev = to_device(case, gpu)
-    # 4096 sequences x 32 heads x 64 partitions of 16 tokens: 4096*32*64*(128+2)*4 bytes >> 32 MiB.
-    status = palib.decode_noalloc_raw(
-        query=dev["query"].data_ptr(), key_cache=dev["key_cache"].data_ptr(),
-        value_cache=dev["value_cache"].data_ptr(), block_tables=dev["block_tables"].data_ptr(),
-        context_lengths=dev["context_lengths"].data_ptr(), output=dev["query"].data_ptr(), batch=4096,
-        query_heads=32, kv_heads=8, head_dim=128, num_blocks=4, block_size=16, max_blocks=64, scale=0.1,
-        dtype=cabi.RK_DTYPE_BF16, index_dtype=cabi.RK_INDEX_INT32, partition_tokens=16, variant=0, stream=0)
-    assert status == cabi.RK_ERR_WORKSPACE
-    assert "scratch" in palib.last_error()

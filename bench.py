@@ -47,6 +47,7 @@ import argparse
 import json
 import math
 import os
+import re
 import statistics
 import sys
 import time
@@ -59,9 +60,11 @@ for entry in (str(ROOT / "radeon-kernels_amd"), str(ROOT)):
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "paged-attn decode µs/call + effective KV GB/s (% MI355X HBM peak), b128"
-# Committed counter summaries of the partition kernel on the 128-sequence workload, one per schedule.
+# Committed counter summaries of the partition kernel: the 128-sequence workload on either schedule and
+# the small workloads; each names the exact configuration it measured.
 TRAFFIC_SUMMARIES = (ROOT / "profiles" / "pa_partition_queue_kernel_b128_traffic.txt",
-                     ROOT / "profiles" / "pa_partition_kernel_b128_traffic.txt")
+                     ROOT / "profiles" / "pa_partition_kernel_b128_traffic.txt",
+                     *sorted((ROOT / "profiles").glob("pa_partition_kernel_*_counters.txt")))
 
 
 def parse_args(argv=None):
@@ -83,6 +86,8 @@ def parse_args(argv=None):
     parser.add_argument("--no-breakdown", action="store_true",
                         help="time only the headline call (no per-kernel breakdown of the other form)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-rk-call", action="store_true",
+                        help="skip timing the public operator (rk_call), e.g. under a profiler")
     parser.add_argument("--append", action="store_true",
                         help="paged_attention_decode: also time one serving step that first appends each "
                              "sequence's new token (position context_length - 1): kv_cache_append then the "
@@ -170,6 +175,14 @@ def read_traffic(workload: str, variant: str, partition: int, merge: str, schedu
     on exactly this configuration: workload, variant, partition size, merge form, schedule and the
     same input draw (its KV bytes per call)."""
 
+    found = read_summary(workload, variant, partition, merge, schedule, kv_bytes)
+    return None if found is None else found[1]
+
+
+def read_summary(workload: str, variant: str, partition: int, merge: str, schedule: str, kv_bytes: int):
+    """(summary path, HBM bytes per launch, kernel-trace average in us or None) of the committed counter
+    summary measured on exactly this configuration, or None."""
+
     for summary in TRAFFIC_SUMMARIES:
         if not summary.is_file():
             continue
@@ -182,7 +195,8 @@ def read_traffic(workload: str, variant: str, partition: int, merge: str, schedu
             if (fields.get("workload") == workload and fields.get("variant") == variant
                     and int(fields["partition_tokens"]) == partition and fields.get("merge", "reduce") == merge
                     and fields.get("schedule", "grid") == schedule and int(fields["kv_bytes_per_call"]) == kv_bytes):
-                return int(fields["hbm_bytes_per_launch"])
+                average = re.search(r"dispatches, average ([0-9.]+) us", summary.read_text())
+                return summary, int(fields["hbm_bytes_per_launch"]), float(average.group(1)) if average else None
         except (KeyError, ValueError):
             continue
     return None
@@ -718,7 +732,8 @@ def main(argv=None) -> int:
     import radeon_kernels as rk
 
     k, v = caches[0]
-    rk_us = public_call_us(torch, lambda: rk.paged_attention_decode(q, k, v, bt, cl), max(1, args.steps // 5))
+    rk_us = None if args.no_rk_call else public_call_us(torch, lambda: rk.paged_attention_decode(q, k, v, bt, cl),
+                                                           max(1, args.steps // 5))
 
     step = None
     if args.append:
@@ -762,7 +777,8 @@ def main(argv=None) -> int:
                 "us_per_step_one_launch": round(one, 2), "entrypoints": ["rk_kv_cache_append + " + PHASE_SYMBOL[headline],
                                                                          "rk_pa_decode_append"]}
 
-    traffic = read_traffic(w.name, variant, partition, merge, schedule, kv_bytes)
+    summary = read_summary(w.name, variant, partition, merge, schedule, kv_bytes)
+    traffic = None if summary is None else summary[1]
     result = {
         "metric": METRIC,
         "value": round(gbps, 1),
@@ -807,13 +823,18 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            # The committed rocprofv3 summary of this configuration (another run, usually another box):
+            # its kernel-trace average and the fraction of peak that average gives.
+            "profile": None if summary is None or summary[2] is None else {
+                "summary": str(summary[0].relative_to(ROOT)), "kernel_avg_us": summary[2],
+                "frac": round(kv_bytes / (summary[2] * 1e3) / HBM_PEAK_GBPS, 4)},
         },
     }
     if hot is not None:
         result["us_per_call_cache_resident"] = hot
     if step is not None:
         result["decode_step_with_append"] = step
-    result["rk_call"] = {"us_per_call": round(rk_us, 2), "selected": decision["selected"],
+    result["rk_call"] = {"us_per_call": None if rk_us is None else round(rk_us, 2), "selected": decision["selected"],
                          "entry_id": decision["entry_id"], "cache_resident": copies > 1}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, data, args.cpu_seconds)

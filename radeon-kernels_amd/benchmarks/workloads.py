@@ -130,6 +130,37 @@ for _case in REFERENCE_CASES:
 REFERENCE_KEYS = tuple(f"{case[0]}-{dtype}" for case in REFERENCE_CASES for dtype in ("fp16", "bf16"))
 
 
+# Shapes sampled from the broad gfx950 dispatch region (paged_attention_decode-gfx950-region), which takes
+# every shape no exact entry names: head layouts from MHA to groups of 16 (8-head chunks), head_dim 64 / 128 /
+# 256, blocks of 8 to 128 tokens (below the 16-token tile too), both dtypes, int32 and int64 indices, fixed
+# and ragged contexts.  The last is the reference's fallback-acceptance shape
+# (developer/promotion/verify_paged_attention_fallback.py:42-47: B=2, 8/2 heads, D=64, block 16), which
+# selects this region on gfx950.  extra["index_dtype"] names the index type the sample is drawn with.
+def _region_sample(name: str, batch: int, hq: int, hkv: int, head_dim: int, block_size: int, dtype: str,
+                   context: int | tuple[int, int], index_dtype: str, seed: int) -> Workload:
+    top = context if isinstance(context, int) else context[1]
+    max_blocks = math.ceil(top / block_size)
+    return Workload(
+        key=f"region-{name}", name=f"region-{name}", batch=batch, query_heads=hq, kv_heads=hkv, head_dim=head_dim,
+        block_size=block_size, dtype=dtype, max_blocks=max_blocks,
+        num_blocks=None if isinstance(context, tuple) else batch * max_blocks, context=context, seed=seed,
+        notes="broad-region sample", extra={"index_dtype": index_dtype})
+
+
+REGION_SAMPLES: tuple[Workload, ...] = (
+    _region_sample("b16-gqa64x8-ragged512to4096-d128-p16-bf16", 16, 64, 8, 128, 16, "bf16", (512, 4096), "int32", 20261301),
+    _region_sample("b8-mha32-c2048-d128-p32-fp16", 8, 32, 32, 128, 32, "fp16", 2048, "int32", 20261302),
+    _region_sample("b32-gqa16x8-ragged100to3000-d64-p8-bf16", 32, 16, 8, 64, 8, "bf16", (100, 3000), "int64", 20261303),
+    _region_sample("b8-gqa16x4-ragged256to2048-d256-p16-fp16", 8, 16, 4, 256, 16, "fp16", (256, 2048), "int32", 20261304),
+    _region_sample("b4-gqa128x8-c8192-d64-p64-bf16", 4, 128, 8, 64, 64, "bf16", 8192, "int32", 20261305),
+    _region_sample("b4-gqa32x8-c4096-d128-p128-bf16", 4, 32, 8, 128, 128, "bf16", 4096, "int64", 20261306),
+    _region_sample("b64-gqa32x8-ragged1to2048-d128-p16-fp16", 64, 32, 8, 128, 16, "fp16", (1, 2048), "int64", 20261307),
+    _region_sample("b2-gqa8x2-ragged41to57-d64-p16-fp16", 2, 8, 2, 64, 16, "fp16", (41, 57), "int32", 20261308),
+)
+for _w in REGION_SAMPLES:
+    WORKLOADS[_w.key] = _w
+
+
 def torch_dtype(torch: Any, name: str) -> Any:
     return {"fp16": torch.float16, "bf16": torch.bfloat16}[name]
 

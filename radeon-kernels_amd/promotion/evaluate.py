@@ -292,6 +292,17 @@ def _announce(message: str) -> None:
     sys.stderr.flush()
 
 
+def _region_entry(operator: str):
+    """(id, launch) of the operator's broad gfx950 region entry."""
+
+    from radeon_kernels.runtime.resources import builtin_dispatch_registry
+
+    manifest = builtin_dispatch_registry().get(operator, "1.0")
+    entry = next(entry for entry in manifest.entries
+                 if entry.environment.architecture == "gfx950" and entry.id.endswith("-region"))
+    return entry.id, dict(entry.launch)
+
+
 def _exact_entries(operator: str):
     from radeon_kernels.runtime.resources import builtin_dispatch_registry
 
@@ -324,10 +335,10 @@ def _guarded_decode(torch, palib, dev, launch, expected_bits) -> bool:
     ct_buf, ct = region(4 * words)
     ct.zero_()
     out_view = out.view(q.dtype).view(q.shape)
-    phase = "fused" if launch.get("merge") == "fused" else "all"
+    phase = "fused" if launch.get("merge") in ("fused", "auto") else "all"  # auto: the library's fused form
     palib.decode(dev["query"], dev["key_cache"], dev["value_cache"], dev["block_tables"], dev["context_lengths"],
                  partition_tokens=partition, out=out_view, workspace=ws if need else None, phase=phase,
-                 counters=ct.view(torch.int32))
+                 counters=ct.view(torch.int32), grow=bool(launch.get("grow_partitions", False)))
     torch.cuda.synchronize()
     intact = all(bool((buf[:guard] == sentinel).all().item()) and bool((buf[-guard:] == sentinel).all().item())
                  for buf in (out_buf, ws_buf, ct_buf))
@@ -336,7 +347,7 @@ def _guarded_decode(torch, palib, dev, launch, expected_bits) -> bool:
 
 def evaluate_paged_attention(torch, samples: int) -> dict:
     import radeon_kernels as rk
-    from benchmarks.workloads import REFERENCE_SEEDS, WORKLOADS, make_inputs
+    from benchmarks.workloads import REFERENCE_SEEDS, REGION_SAMPLES, WORKLOADS, make_inputs
     from radeon_kernels import cabi
     from radeon_kernels.cabi import library
     from radeon_kernels.ops.paged_attention.reference import paged_attention_decode_reference as fallback
@@ -357,15 +368,18 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
         return torch.cat(outs)
 
     cases, entries = [], {}
-    for entry_id, suffix, launch in _exact_entries("paged_attention_decode"):
-        w = WORKLOADS[PA_RAGGED.get(suffix, suffix)]
-        seeds = REFERENCE_SEEDS if w.distribution == "uniform" else tuple(range(w.seed, w.seed + SEEDS_PER_CASE))
+
+    def check_cases(w, seeds, entry_id, launch, label):
+        """Correctness of the public operator on ``w`` for every seed (it must select ``entry_id``);
+        returns the first seed's inputs, kept for the timing."""
+
         first = None
+        index_dtype = w.extra.get("index_dtype", "int32")
         for seed in seeds:
-            data = make_inputs(w, seed=seed, device=device)
+            data = make_inputs(w, seed=seed, device=device, index_dtype=index_dtype)
             args = (data["query"], data["key_cache"], data["value_cache"], data["block_tables"],
                     data["context_lengths"])
-            _announce(f"paged_attention_decode {suffix} seed {seed}")
+            _announce(f"paged_attention_decode {label} seed {seed}")
             out = rk.paged_attention_decode(*args)
             record = rk.get_last_dispatch()
             expected = reference_fp32(data, 4 if w.ragged else w.batch)
@@ -373,7 +387,7 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
             finite = bool(torch.isfinite(out).all().item())
             runtime_ok = record["selected"] == "native/decode_mfma" and record["entry_id"] == entry_id
             guards = _guarded_decode(torch, palib, data, launch, out.view(torch.int16))
-            cases.append({"case_id": f"{suffix}-seed{seed}", "workload": suffix, "seed": seed, "dtype": w.dtype,
+            cases.append({"case_id": f"{label}-seed{seed}", "workload": label, "seed": seed, "dtype": w.dtype,
                           "runtime_ok": runtime_ok, "finite": finite, "guards_intact": guards,
                           "max_absolute_error": error, "tolerance": TOLERANCE[w.dtype], "entry_id": entry_id,
                           "passed": runtime_ok and finite and guards and error <= TOLERANCE[w.dtype]})
@@ -383,8 +397,11 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
             else:
                 del data
             torch.cuda.empty_cache()
+        return first
 
-        data = first
+    def paired_timing(data, w, launch, label):
+        """The entry's launch through its C-ABI entry point from a C loop against the fallback, paired."""
+
         cache_bytes = data["key_cache"].numel() * data["key_cache"].element_size() * 2
         q, bt, cl = data["query"], data["block_tables"], data["context_lengths"]
         batch, hq, d = (int(x) for x in q.shape)
@@ -394,10 +411,11 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
         out = torch.empty_like(q)
         ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
         counters = torch.zeros(palib.counter_words(batch, hq, hkv), dtype=torch.int32, device=device)
-        fused = launch.get("merge") == "fused"
+        fused = launch.get("merge") in ("fused", "auto")
         symbol = palib.lib.rk_pa_decode_fused if fused else palib.lib.rk_pa_decode
         dtype_code = cabi.RK_DTYPE_BF16 if q.dtype == torch.bfloat16 else cabi.RK_DTYPE_FP16
         index_code = cabi.RK_INDEX_INT64 if bt.dtype == torch.int64 else cabi.RK_INDEX_INT32
+        variant = cabi.VARIANTS["mfma"] | (cabi.RK_PA_PARTITION_GROW if launch.get("grow_partitions") else 0)
 
         def launch_for(caches, out=out, q=q, bt=bt, cl=cl, ws=ws, need=need, counters=counters, fused=fused,
                        symbol=symbol, partition=partition, nb=int(data["key_cache"].shape[0]), dtype_code=dtype_code,
@@ -409,8 +427,7 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
                     loops.address(symbol), n, first, len(caches), q.data_ptr(), kptrs, vptrs, bt.data_ptr(),
                     cl.data_ptr(), out.data_ptr(), ws.data_ptr() if need else None, need,
                     counters.data_ptr() if fused else None, counters.numel() if fused else 0, batch, hq, hkv, d, nb,
-                    bs, int(bt.shape[1]), scale, dtype_code, index_code, partition, cabi.VARIANTS["mfma"],
-                    stream_handle)
+                    bs, int(bt.shape[1]), scale, dtype_code, index_code, partition, variant, stream_handle)
                 palib.check(status)
 
             return run
@@ -437,7 +454,7 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
         caches = first_copy + [(data["key_cache"].clone(), data["value_cache"].clone()) for _ in range(copies - 1)]
         candidate = Side(torch, candidate_calls(caches), copies, graph_c, "candidate")
         baseline = Side(torch, per_call(baseline_for(caches), copies), copies, graph_b, "baseline")
-        _announce(f"paged_attention_decode {suffix} timing ({copies} copies, graphs: {graph_c}/{graph_b})")
+        _announce(f"paged_attention_decode {label} timing ({copies} copies, graphs: {graph_c}/{graph_b})")
         timing = time_pair(torch, candidate, baseline, samples=samples, copies=copies)
         timing["baseline_method"] = (f"{METHODS['paged_attention_decode']}"
                                      + (f" ({chunk}-sequence chunks)" if chunk < batch else ""))
@@ -448,8 +465,28 @@ def evaluate_paged_attention(torch, samples: int) -> dict:
             launch_for(first_copy)(0, 1, stream.cuda_stream)
             torch.cuda.synchronize()
             timing["graph_replay_matches_eager"] = bool(torch.equal(replay.view(torch.int16), out.view(torch.int16)))
-        entries[entry_id] = {"workload": suffix, "launch": launch, "timing": timing}
-        del caches, data, first, candidate, baseline
+        del caches, candidate, baseline
+        return timing
+
+    for entry_id, suffix, launch in _exact_entries("paged_attention_decode"):
+        w = WORKLOADS[PA_RAGGED.get(suffix, suffix)]
+        seeds = REFERENCE_SEEDS if w.distribution == "uniform" else tuple(range(w.seed, w.seed + SEEDS_PER_CASE))
+        data = check_cases(w, seeds, entry_id, launch, suffix)
+        entries[entry_id] = {"workload": suffix, "launch": launch, "timing": paired_timing(data, w, launch, suffix)}
+        del data
+        torch.cuda.empty_cache()
+
+    # The broad region: sampled shapes no exact entry names, each checked and timed like an exact entry.
+    region_id, region_launch = _region_entry("paged_attention_decode")
+    for w in REGION_SAMPLES:
+        data = check_cases(w, tuple(range(w.seed, w.seed + SEEDS_PER_CASE)), region_id, region_launch, w.key)
+        shape = {"dtype": w.dtype, "batch": w.batch, "query_heads": w.query_heads, "kv_heads": w.kv_heads,
+                 "head_dim": w.head_dim, "block_size": w.block_size, "max_blocks_per_sequence": w.max_blocks,
+                 "context": f"{w.context[0]}..{w.context[1]}" if w.ragged else w.context,
+                 "index_dtype": w.extra.get("index_dtype", "int32")}
+        entries[f"{region_id}/{w.key}"] = {"workload": w.key, "launch": region_launch, "region_sample": shape,
+                                           "timing": paired_timing(data, w, region_launch, w.key)}
+        del data
         torch.cuda.empty_cache()
 
     headline = f"paged_attention_decode-gfx950-{HEADLINE['paged_attention_decode']}"

@@ -361,6 +361,42 @@ def proposal_for(operator: str, evaluation_path: Path) -> dict[str, Any]:
                 f"Exact {pack_env.architecture}, ROCm {pack_env.rocm_abi}, {pack_env.python_abi}, PyTorch "
                 f"{pack_env.pytorch_version}; the gfx950 dispatch entry {entry_id}; contiguous inference only."),
         })
+    # The broad region, when the evaluation sampled it: one record over all its sampled shapes (timing on the
+    # first) and one per sampled shape with that shape's cases and paired timing.
+    for region_id in sorted(entry.id for entry in gfx950 if entry.id.endswith("-region")):
+        samples = [key for key in evaluation.get("entries", {}) if key.startswith(region_id + "/")]
+        if not samples:
+            continue
+        region_cases = [case for case in public_evidence["correctness"]["cases"]
+                        if case_entry.get(case["case_id"]) == region_id]
+        names = [evaluation["entries"][key]["workload"] for key in samples]
+        correctness = {"passed": all(c["passed"] for c in evaluation["cases"] if c["entry_id"] == region_id),
+                       "oracle": evaluation["oracle"], "cases": region_cases}
+        boundary = (f"Exact {pack_env.architecture}, ROCm {pack_env.rocm_abi}, {pack_env.python_abi}, PyTorch "
+                    f"{pack_env.pytorch_version}; the gfx950 dispatch entry {region_id}")
+        entry_evidence.append({
+            **public_evidence,
+            "evidence_id": f"{item.evidence_id}.{region_id[len(prefix):]}",
+            "workload": {**_scalar_workload(raw_entries[region_id]["workload"]),
+                         "evidence_scope": (f"{len(samples)} sampled shapes of the region ({', '.join(names)}): "
+                                            f"correctness on every one, timing on {names[0]} (each shape's timing in "
+                                            f"its own record)")},
+            "correctness": correctness,
+            "timing": per_entry[samples[0]],
+            "guarantee_boundary": boundary + "; the sampled shapes named in the workload; contiguous inference only.",
+        })
+        for key, name in zip(samples, names):
+            cases_here = [case for case in region_cases if case["case_id"].startswith(name + "-seed")]
+            entry_evidence.append({
+                **public_evidence,
+                "evidence_id": f"{item.evidence_id}.{name}",
+                "workload": {**evaluation["entries"][key]["region_sample"], "evidence_scope": f"sampled from {region_id}"},
+                "correctness": {"passed": all(c["passed"] for c in evaluation["cases"]
+                                              if c["entry_id"] == region_id and c["workload"] == name),
+                                "oracle": evaluation["oracle"], "cases": cases_here},
+                "timing": per_entry[key],
+                "guarantee_boundary": boundary + f", on the sampled shape {name}; contiguous inference only.",
+            })
     identity = _sha256(json.dumps({"evidence_id": item.evidence_id, "sources": sources},
                                   sort_keys=True).encode())[:16]
     return {

@@ -16,9 +16,10 @@ signatures written here verify there and the reference's published signatures ve
 The Ed25519 arithmetic is radeon_kernels.runtime.ed25519 (RFC 8032, pure Python), standing in for
 the ``cryptography`` package the reference imports.
 
-The built-in keyring (radeon_kernels/keys/trusted-keys.json) holds the reference's release key
-(public data from its keys/trusted-keys.json, so its signed packs verify) and this build's gfx950
-development key.
+The built-in keyring (radeon_kernels/keys/trusted-keys.json) holds release keys only: the reference's
+release key (public data from its keys/trusted-keys.json, so its signed packs verify) and the gfx950
+pack's release key.  A development key is trusted only through a separate keyring that
+RADEON_KERNELS_DEV_TRUSTED_KEYS names, and never shadows a built-in key id.
 """
 
 from __future__ import annotations

@@ -104,13 +104,17 @@ def candidate_record(operator: str) -> dict:
 
     artifact = {"paged_attention_decode": dispatch_plan.ARTIFACT, "kv_cache_append": dispatch_plan.KV_ARTIFACT,
                 "kv_cache_copy": dispatch_plan.KV_COPY_ARTIFACT, "sdpa": dispatch_plan.SDPA_ARTIFACT}[operator]
-    library, source = {"paged_attention_decode": ("librk_pa_gfx950.so", "pa_decode_gfx950.hip"),
-                       "sdpa": ("librk_sdpa_gfx950.so", "sdpa_gfx950.hip")}.get(
-        operator, ("librk_kv_gfx950.so", "kv_cache_gfx950.hip"))
+    library, sources = {"paged_attention_decode": ("librk_pa_gfx950.so", ("pa_decode_gfx950.hip", "pa_decode_kernels.hip",
+                                                                          "pa_decode_common.hpp")),
+                        "sdpa": ("librk_sdpa_gfx950.so", ("sdpa_gfx950.hip",))}.get(
+        operator, ("librk_kv_gfx950.so", ("kv_cache_gfx950.hip",)))
     pack = PACKAGE_ROOT / "packs" / "gfx950"
+    # One source: its SHA-256.  Several: the SHA-256 of their "name sha256" lines, in the order listed.
+    digests = [(name, sha256_file(PACKAGE_ROOT / "csrc" / name)) for name in sources]
+    source_sha256 = digests[0][1] if len(digests) == 1 else sha256_bytes(
+        "".join(f"{name} {digest}\n" for name, digest in digests).encode())
     return {"artifact": artifact, "artifact_sha256": sha256_file(pack / artifact),
-            "library_sha256": sha256_file(pack / "lib" / library),
-            "source_sha256": sha256_file(PACKAGE_ROOT / "csrc" / source)}
+            "library_sha256": sha256_file(pack / "lib" / library), "source_sha256": source_sha256}
 
 
 def rotation_copies(nbytes: int) -> int:

@@ -170,16 +170,18 @@ def dispatch_launch(torch, q, k, v, bt, cl) -> dict:
     return rk.get_last_dispatch()
 
 
-def read_traffic(workload: str, variant: str, partition: int, merge: str, schedule: str, kv_bytes: int):
+def read_traffic(workload: str, variant: str, partition: int, merge: str, schedule: str, kv_bytes: int,
+                 seed: int | None = None):
     """HBM bytes per partition-kernel launch from a committed counter summary, if one was measured
     on exactly this configuration: workload, variant, partition size, merge form, schedule and the
-    same input draw (its KV bytes per call)."""
+    same input draw (its KV bytes per call, and its seed where the summary records one)."""
 
-    found = read_summary(workload, variant, partition, merge, schedule, kv_bytes)
+    found = read_summary(workload, variant, partition, merge, schedule, kv_bytes, seed)
     return None if found is None else found[1]
 
 
-def read_summary(workload: str, variant: str, partition: int, merge: str, schedule: str, kv_bytes: int):
+def read_summary(workload: str, variant: str, partition: int, merge: str, schedule: str, kv_bytes: int,
+                 seed: int | None = None):
     """(summary path, HBM bytes per launch, kernel-trace average in us or None) of the committed counter
     summary measured on exactly this configuration, or None."""
 
@@ -194,7 +196,8 @@ def read_summary(workload: str, variant: str, partition: int, merge: str, schedu
         try:
             if (fields.get("workload") == workload and fields.get("variant") == variant
                     and int(fields["partition_tokens"]) == partition and fields.get("merge", "reduce") == merge
-                    and fields.get("schedule", "grid") == schedule and int(fields["kv_bytes_per_call"]) == kv_bytes):
+                    and fields.get("schedule", "grid") == schedule and int(fields["kv_bytes_per_call"]) == kv_bytes
+                    and ("seed" not in fields or seed is None or int(fields["seed"]) == seed)):
                 average = re.search(r"dispatches, average ([0-9.]+) us", summary.read_text())
                 return summary, int(fields["hbm_bytes_per_launch"]), float(average.group(1)) if average else None
         except (KeyError, ValueError):
@@ -777,7 +780,7 @@ def main(argv=None) -> int:
                 "us_per_step_one_launch": round(one, 2), "entrypoints": ["rk_kv_cache_append + " + PHASE_SYMBOL[headline],
                                                                          "rk_pa_decode_append"]}
 
-    summary = read_summary(w.name, variant, partition, merge, schedule, kv_bytes)
+    summary = read_summary(w.name, variant, partition, merge, schedule, kv_bytes, data["seed"])
     traffic = None if summary is None else summary[1]
     result = {
         "metric": METRIC,

@@ -95,6 +95,10 @@ def test_bench_reads_traffic_only_for_its_exact_configuration(tmp_path, monkeypa
     assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "queue", kv) == 4_867_000_000
     assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "grid", kv) is None
     assert bench.read_traffic("b128-x", "mfma", 2048, "reduce", "queue", kv) is None
+    # A summary that records its draw's seed matches that seed only (same shape and KV bytes, other values).
+    summary.write_text(summary.read_text() + "seed = 7\n")
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "queue", kv, seed=7) == 4_867_000_000
+    assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "queue", kv, seed=8) is None
     monkeypatch.setattr(bench, "TRAFFIC_SUMMARIES", (tmp_path / "absent.txt",))
     assert bench.read_traffic("b128-x", "mfma", 2048, "fused", "queue", kv) is None
 

@@ -682,10 +682,12 @@ def main(argv=None) -> int:
         wall = time.perf_counter() - t
         return start.elapsed_time(end) * 1e3 / args.steps, wall * 1e6 / args.steps
 
-    # The timed regions.  Every form bench reports is timed as S interleaved samples of K launches
-    # (the reference's protocol: paired, order-alternating samples, benchmark.py:221-229 with the
-    # workload file's 30 samples and 3% CV gate, benchmarks/workloads/paged_attention_decode-1.0.yaml:8-11):
-    # sample s runs the headline form (K whole decode calls, nothing else on the stream), then the
+    # The timed regions.  Every form bench reports is timed as S interleaved samples of K launches,
+    # after the reference's protocol of paired, order-alternating samples (benchmark.py:221-229; its
+    # workload file asks for 30 samples and a CV of at most 3%,
+    # benchmarks/workloads/paged_attention_decode-1.0.yaml:8-11; S defaults to 10 here so the default run
+    # stays short, and the headline's CV is reported): sample s runs the headline form (K whole decode
+    # calls, nothing else on the stream), then the
     # reduce form's partition kernel and merge kernel alone, then the other whole-call form, and
     # sample s + 1 runs them in the reverse order, so no form always runs first.  value, ms_per_step
     # and roofline.frac are medians over the headline samples.  In the fused form the call is the

@@ -38,13 +38,15 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-// Query heads per workgroup: 8 for groups of 8 or more at head_dim 64 and 128 (measured 1.3-1.75x faster
-// than two chunks of 4 there), else up to 4.  At head_dim 256 the 8-head form is not built: with PV on
-// fp32 FMAs its accumulators spill.
-int head_chunk_for(int64_t group, int64_t head_dim) {
+// Query heads per workgroup: 8 for groups of 8 or more (each KV row is then read once per 8 query
+// heads), else up to 4.  At head_dim 64 and 128 that held for every variant (1.3-1.75x faster than two
+// chunks of 4).  At head_dim 256 it holds only with PV on MFMA, where a lane keeps 4 of the 8 heads'
+// accumulators; with PV on fp32 FMAs the 8-head accumulators spill there, and those variants keep
+// chunks of 4 (their 8-head head_dim 256 kernels are not built).
+int head_chunk_for(int64_t group, int64_t head_dim, int variant) {
   if (group == 1) return 1;
   if (group == 2) return 2;
-  return group >= 8 && head_dim <= 128 ? 8 : 4;
+  return group >= 8 && (head_dim <= 128 || variant == RK_PA_VARIANT_MFMA) ? 8 : 4;
 }
 
 int log2_exact(int64_t x) {
@@ -340,7 +342,7 @@ int decode_phases(const void* query, const void* key_cache, const void* value_ca
   }
 
   const int64_t group = query_heads / kv_heads;
-  const int gc = head_chunk_for(group, head_dim);
+  const int gc = head_chunk_for(group, head_dim, variant);
   const int64_t head_chunks = (group + gc - 1) / gc;
   const int64_t grid = batch * kv_heads * head_chunks * s.num_partitions;  // one workgroup per work item
   if (grid >= (int64_t{1} << 31))
@@ -550,7 +552,7 @@ extern "C" int rk_pa_decode_schedule(int64_t batch, int64_t query_heads, int64_t
   const bool queue = requested != kScheduleGrid && queue_eligible(s, variant);
   if (requested == kScheduleQueue && !queue) return queue_unsupported();
   const int64_t group = query_heads / kv_heads;
-  const int gc = head_chunk_for(group, head_dim);
+  const int gc = head_chunk_for(group, head_dim, variant);
   const int64_t rows = queue && batch > kQueueMaxBatch ? kQueueMaxBatch : batch;  // the first launch
   const int64_t items = rows * kv_heads * ((group + gc - 1) / gc) * s.num_partitions;
   Params prm{};

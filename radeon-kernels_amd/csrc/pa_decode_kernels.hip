@@ -403,7 +403,8 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
 //           128 (one wave per SIMD) and the chunk still measured 1.32-1.67x faster than two chunks
 //           of 4; with PV on MFMA a lane holds 4 of the 8 heads' accumulators and the chunk runs at
 //           two waves per SIMD.  At head_dim 64 the 8-head chunk measured 1.6-1.75x faster than
-//           two chunks of 4 (128x8 and 64x8 layouts)
+//           two chunks of 4 (128x8 and 64x8 layouts).  At head_dim 256 it is built with PV on MFMA
+//           only (with PV on fp32 FMAs its accumulators spill)
 //   QK_MFMA QK^T on MFMA (true) or on fp32 FMAs + DPP row sums (false)
 //   PV_MFMA PV on MFMA as well (QK_MFMA only): the probabilities leave the QK^T MFMA in exactly the
 //           A-operand layout of a 16x16x32 MFMA (lane 16g + j: score column j, tokens 4g..4g+3), and
@@ -1503,12 +1504,20 @@ hipError_t launch_partition_ub(const Params& prm, const Launch& l) {
 template <class E, int D, int GC>
 hipError_t launch_partition(const Params& prm, int variant, const Launch& l) {
   const bool pv_mfma = variant == RK_PA_VARIANT_MFMA;
-  if (prm.new_k != nullptr)  // validated: an MFMA variant
-    return pv_mfma ? launch_partition_ub<E, D, GC, true, true, true>(prm, l)
-                   : launch_partition_ub<E, D, GC, true, false, true>(prm, l);
-  if (pv_mfma) return launch_partition_ub<E, D, GC, true, true, false>(prm, l);
-  if (variant == RK_PA_VARIANT_MFMA_QK) return launch_partition_ub<E, D, GC, true, false, false>(prm, l);
-  return launch_partition_ub<E, D, GC, false, false, false>(prm, l);
+  if constexpr (D == 256 && GC == 8) {
+    // Built with PV on MFMA only: with PV on fp32 FMAs the 8-head accumulators spill at head_dim 256,
+    // and the host gives those variants chunks of 4.
+    if (!pv_mfma) return hipErrorInvalidValue;
+    if (prm.new_k != nullptr) return launch_partition_ub<E, D, GC, true, true, true>(prm, l);
+    return launch_partition_ub<E, D, GC, true, true, false>(prm, l);
+  } else {
+    if (prm.new_k != nullptr)  // validated: an MFMA variant
+      return pv_mfma ? launch_partition_ub<E, D, GC, true, true, true>(prm, l)
+                     : launch_partition_ub<E, D, GC, true, false, true>(prm, l);
+    if (pv_mfma) return launch_partition_ub<E, D, GC, true, true, false>(prm, l);
+    if (variant == RK_PA_VARIANT_MFMA_QK) return launch_partition_ub<E, D, GC, true, false, false>(prm, l);
+    return launch_partition_ub<E, D, GC, false, false, false>(prm, l);
+  }
 }
 
 template <class E, int D>
@@ -1519,8 +1528,6 @@ hipError_t launch_all(const Params& prm, int gc, int variant, const Launch& l, b
       err = launch_partition<E, D, 1>(prm, variant, l);
     else if (gc == 2)
       err = launch_partition<E, D, 2>(prm, variant, l);
-    else if constexpr (D == 256)
-      err = launch_partition<E, D, 4>(prm, variant, l);
     else if (gc == 4)
       err = launch_partition<E, D, 4>(prm, variant, l);
     else

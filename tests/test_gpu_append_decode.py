@@ -94,6 +94,7 @@ SHAPES = [
     (64, 8, 128, 16, "fp16"),   # group 8: one 8-head chunk, which stores
     (128, 8, 64, 16, "bf16"),   # group 16: two 8-head chunks, the first one stores
     (32, 8, 256, 16, "bf16"),
+    (64, 8, 256, 16, "fp16"),   # group 8 at head_dim 256: one 8-head chunk (PV on MFMA)
     (4, 4, 256, 8, "fp16"),     # blocks smaller than a tile
     (8, 2, 128, 1, "fp16"),     # one token per block
 ]

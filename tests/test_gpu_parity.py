@@ -75,7 +75,8 @@ SHAPES = [
     (64, 8, 128, 16, "fp16"),   # group 8: one 8-head chunk (8-lane probability broadcast)
     (128, 8, 64, 16, "bf16"),   # group 16: two 8-head chunks
     (24, 2, 128, 32, "fp16"),   # group 12: an 8-head chunk, then 4 heads in an 8-head chunk
-    (64, 8, 256, 16, "bf16"),   # group 8 at head_dim 256: two 4-head chunks
+    (64, 8, 256, 16, "bf16"),   # group 8 at head_dim 256: one 8-head chunk (mfma), two chunks of 4 (others)
+    (128, 8, 256, 16, "fp16"),  # group 16 at head_dim 256: two 8-head chunks (mfma), four chunks of 4
     (32, 8, 256, 16, "bf16"),
     (4, 4, 256, 8, "fp16"),
     (32, 4, 128, 64, "bf16"),

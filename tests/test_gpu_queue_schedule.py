@@ -40,7 +40,8 @@ def ragged_contexts(batch, limit, seed):
 
 
 # (query_heads, kv_heads, head_dim, block_size, dtype, index_dtype, partition): head chunks of 4, 1,
-# 2 and 8 and two chunks of 4 (group 8 at head_dim 256); blocks of 16, 32, 8 and 1 tokens; every head_dim.
+# 2 and 8 (group 8 at head_dim 256: one chunk of 8 with PV on MFMA, two chunks of 4 otherwise); blocks of
+# 16, 32, 8 and 1 tokens; every head_dim.
 SHAPES = [
     (32, 8, 128, 16, "bf16", "int32", 128),
     (16, 16, 64, 32, "bf16", "int64", 64),

@@ -141,7 +141,7 @@ int rk_pa_decode_workspace_bytes(int64_t batch, int64_t query_heads, int64_t hea
  * Paged-attention decode: one query token per sequence against the paged K/V cache.
  *
  * partition_tokens: context tokens per workgroup (split-K partition); a multiple of 16 in
- *   [16, 8192] with partition_tokens / block_size <= 256.
+ *   [16, 8192] with partition_tokens / block_size <= 512.
  * variant: RK_PA_VARIANT_MFMA, RK_PA_VARIANT_VALU or RK_PA_VARIANT_MFMA_QK, optionally OR-ed with one RK_PA_SCHEDULE_* bit
  *   and with RK_PA_PARTITION_GROW.
  * workspace/workspace_bytes: device buffer of at least rk_pa_decode_workspace_bytes(...) bytes

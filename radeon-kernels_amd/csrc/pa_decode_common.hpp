@@ -14,7 +14,15 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kTile = 16;             // tokens per wave step = MFMA M
-constexpr int kMaxSliceBlocks = 257;  // partition_tokens / block_size <= 256, plus one straddle
+// Block-table entries of one partition's slice.  The host admits partition_tokens / block_size <=
+// 512.  For block sizes up to 16 the partition size is a multiple of the block size, so a slice holds
+// exactly partition_tokens / block_size entries; for larger blocks partition_tokens <= 8192 keeps it
+// to 8192 / 32 + 1 = 257, the one extra entry being a block that straddles the partition start.
+constexpr int kMaxSliceBlocks = 512;
+// Partition growth stops at 256 blocks per partition.  Growth is balanced on sizes up to that many
+// blocks; wider slices serve explicit partition sizes such as the 8192-token partitions of long
+// 16-token-block contexts.
+constexpr int kGrowMaxSliceBlocks = 256;
 // Work-queue schedule limits: sequences and partition levels whose item map fits in LDS.
 constexpr int kQueueMaxBatch = 1024;
 constexpr int kQueueMaxLevels = 256;

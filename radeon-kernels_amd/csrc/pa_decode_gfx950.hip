@@ -76,8 +76,8 @@ int check_shape(const Shape& s) {
     return fail(RK_ERR_INVALID_ARGUMENT,
                 "partition_tokens must be a multiple of 16 in [16, 8192] (got %lld)",
                 static_cast<long long>(s.partition));
-  if (s.partition / s.block_size > kMaxSliceBlocks - 1)
-    return fail(RK_ERR_INVALID_ARGUMENT, "partition_tokens / block_size must be <= 256");
+  if (s.partition / s.block_size > kMaxSliceBlocks)
+    return fail(RK_ERR_INVALID_ARGUMENT, "partition_tokens / block_size must be <= %d", kMaxSliceBlocks);
   if (16 * s.kv_heads * s.head_dim >= (int64_t{1} << 30))
     return fail(RK_ERR_UNSUPPORTED, "kv_heads * head_dim is too large for this kernel");
   if (s.num_blocks >= (int64_t{1} << 31) || s.max_blocks * s.block_size >= (int64_t{1} << 31) ||
@@ -255,7 +255,7 @@ void grow_base(Shape* s, int variant, int schedule, bool grow) {
   int64_t base = s->partition;
   while ((table_tokens + base - 1) / base > kQueueMaxLevels) {
     base *= 2;
-    if (base > kGrowMaxTokens || base / s->block_size > kMaxSliceBlocks - 1) return;
+    if (base > kGrowMaxTokens || base / s->block_size > kGrowMaxSliceBlocks) return;
   }
   s->partition = base;
   s->num_partitions = partitions_for(*s);
@@ -269,7 +269,7 @@ int32_t grow_limit(const Shape& s) {
   int64_t limit = s.partition;
   for (int k = 0; k < kGrowMaxSteps; ++k) {
     const int64_t next = limit * 2;
-    if (next > kGrowMaxTokens || next / s.block_size > kMaxSliceBlocks - 1 || next >= table_tokens) break;
+    if (next > kGrowMaxTokens || next / s.block_size > kGrowMaxSliceBlocks || next >= table_tokens) break;
     limit = next;
   }
   return limit > s.partition ? static_cast<int32_t>(limit) : 0;

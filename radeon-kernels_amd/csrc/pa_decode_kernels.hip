@@ -503,7 +503,8 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   const int64_t table_row = static_cast<int64_t>(b) * p.max_blocks + blk0;
   const bool is64 = p.index_is64 != 0;
   const RawIndex ctx_raw = load_raw_index(p.context_lengths, b, is64);
-  RawIndex ids[2] = {{~0u, ~0u}, {~0u, ~0u}};  // entries tid and tid + kThreads (a slice has <= 257)
+  static_assert(2 * kThreads >= kMaxSliceBlocks, "two table entries per thread cover a partition's slice");
+  RawIndex ids[2] = {{~0u, ~0u}, {~0u, ~0u}};  // entries tid and tid + kThreads (a slice has <= 512)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int idx = tid + i * kThreads;

@@ -105,10 +105,11 @@ EXACT_REGIONS: list[tuple[str, dict[str, Any], dict[str, Any]]] = [
         "b128-gqa32x8-ragged-d128-p16-bf16",
         {"dtype": "bf16", "batch": 128, "query_heads": 32, "kv_heads": 8, "head_dim": 128,
          "num_blocks": [1, _INT_MAX], "block_size": 16, "max_blocks_per_sequence": 1024},
-        # Work-queue schedule (the library's choice for its 8192 work items): partitions of 4096
-        # tokens, the table's limit at 16-token blocks, measured fastest (646.8 us per call against
-        # 656.6 at 2048 and 651.9 at 3072, fused).
-        {"partition_tokens": 4096, "merge": "fused"},
+        # Work-queue schedule (the library's choice for this batch): partitions of 8192 tokens, the
+        # largest size the library takes, measured fastest, fused.  Five separately allocated call
+        # instances each (workspace, counters, output) ran 642.8-646.2 us per call against
+        # 644.3-659.2 at 4096; 6144 ran 652.1 and, earlier, 3072 651.9 and 2048 656.6.
+        {"partition_tokens": 8192, "merge": "fused"},
     ),
 ]
 

@@ -131,7 +131,7 @@ def call(lib, **overrides):
         (dict(block_size=512), cabi.RK_ERR_UNSUPPORTED, "power of two"),
         (dict(partition_tokens=40), cabi.RK_ERR_INVALID_ARGUMENT, "multiple of 16"),
         (dict(partition_tokens=8192 * 2), cabi.RK_ERR_INVALID_ARGUMENT, "multiple of 16"),
-        (dict(partition_tokens=8192, block_size=16), cabi.RK_ERR_INVALID_ARGUMENT, "<= 256"),
+        (dict(partition_tokens=8192, block_size=8), cabi.RK_ERR_INVALID_ARGUMENT, "<= 512"),
         (dict(batch=0), cabi.RK_ERR_INVALID_ARGUMENT, "positive"),
         (dict(num_blocks=1 << 31), cabi.RK_ERR_UNSUPPORTED, "32-bit"),
         (dict(kv_heads=1 << 19, query_heads=1 << 19), cabi.RK_ERR_UNSUPPORTED, "too large"),

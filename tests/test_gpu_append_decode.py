@@ -107,8 +107,8 @@ def test_shape_sweep(gpu, palib, kvlib, shape, partition, phase):
     import torch
 
     hq, hkv, d, bs, dtype = shape
-    if partition // bs > 256:
-        pytest.skip("partition_tokens / block_size must be <= 256")
+    if partition // bs > 512:
+        pytest.skip("partition_tokens / block_size must be <= 512")
     # Empty context (nothing appended, NaN row), one token, block and partition boundaries, ragged.
     contexts = [0, 1, bs, bs + 1, 16, 65, 300, 1024 + 7]
     case = make_case(torch, batch=len(contexts), query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bs,

@@ -60,7 +60,7 @@ def test_public_api_ragged_b128_selects_exact_entry(gpu, c5_case):
     record = rk.get_last_dispatch()
     assert record["selected"] == "native/decode_mfma"
     assert record["entry_id"] == "paged_attention_decode-gfx950-b128-gqa32x8-ragged-d128-p16-bf16"
-    assert record["launch"] == {"partition_tokens": 4096, "merge": "fused"}
+    assert record["launch"] == {"partition_tokens": 8192, "merge": "fused"}
     assert_within(out, c5_case["expected"], "bf16", "public c5 call, all 128 rows")
 
 

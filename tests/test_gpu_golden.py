@@ -85,7 +85,7 @@ def test_binding_both_merge_forms_match_golden(gpu, name, variant):
     # 16-token partitions split every sequence (records and a merge); one partition covering the
     # whole table needs no merge at all.
     for partition in sorted({16, max(16, -(-table_tokens // 16) * 16)}):
-        if partition // block_size > 256:
+        if partition // block_size > 512:
             continue
         for merge in ("fused", "reduce"):
             announce(f"golden {name} variant={variant} partition={partition} merge={merge}")

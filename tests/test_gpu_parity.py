@@ -67,6 +67,42 @@ def test_partition_sizes_agree(gpu, palib, partition, variant):
     assert_within(out, oracle64(case), "bf16", f"partition {partition}")
 
 
+@pytest.mark.parametrize("block_size, partition, contexts, table", [
+    (16, 8192, [16384, 12000, 8191, 8192, 8193, 100, 0], 16384),  # the b128 entry's partitions
+    (8, 4096, [8192, 5000, 4095, 4097, 1], 8192),                 # per-lane table reads (blocks < 16)
+    (1, 512, [1024, 700, 511, 513, 2], 1024),
+])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_slices_of_512_blocks(gpu, palib, block_size, partition, contexts, table, dtype):
+    """Partitions of 512 table entries, the widest slice the library takes: every schedule and merge
+    form of the MFMA variant, and the two-launch form of the others, against the float64 oracle.  The
+    MFMA forms must agree bit for bit."""
+
+    import torch
+    from test_gpu_partition_growth import device_case
+
+    d = device_case(gpu, batch=len(contexts), contexts=contexts, table_tokens=table, dtype=dtype,
+                    seed=block_size + partition, block_size=block_size)
+    args = [d[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    expected = oracle64(d)
+    live = torch.tensor(contexts) > 0
+    outs = {}
+    for variant, phase, schedule in (("mfma", "all", "grid"), ("mfma", "all", "queue"), ("mfma", "fused", "grid"),
+                                     ("mfma", "fused", "queue"), ("mfma_qk", "all", "grid"), ("valu", "all", "grid")):
+        tag = f"bs{block_size} P{partition} {dtype} {variant} {phase} {schedule}"
+        announce(tag)
+        counters = torch.zeros(palib.counter_words(len(contexts), 32, 8), dtype=torch.int32, device=gpu)
+        out = palib.decode(*args, partition_tokens=partition, variant=variant, phase=phase, schedule=schedule,
+                           counters=counters if phase == "fused" else None).cpu()
+        assert torch.isnan(out[~live]).all(), tag
+        assert_within(out[live], expected[live.numpy()], dtype, tag)
+        outs[variant, phase, schedule] = out
+    reference = outs["mfma", "all", "grid"].view(torch.int16)
+    for key, out in outs.items():
+        if key[0] == "mfma":
+            assert torch.equal(out.view(torch.int16), reference), key
+
+
 SHAPES = [
     # (Hq, Hkv, D, BS, dtype)
     (8, 8, 64, 16, "fp16"),
@@ -222,8 +258,8 @@ def test_fused_shape_sweep(gpu, palib, shape, partition, variant):
     import torch
 
     hq, hkv, d, bs, dtype = shape
-    if partition // bs > 256:
-        pytest.skip("partition_tokens / block_size must be <= 256")
+    if partition // bs > 512:
+        pytest.skip("partition_tokens / block_size must be <= 512")
     case = make_case(torch, batch=3, query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bs,
                      contexts=[5, bs * 3 + 1, 1500], dtype=dtype, seed=hq * 5 + d + bs)
     dev = to_device(case, gpu)

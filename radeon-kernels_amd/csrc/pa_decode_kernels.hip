@@ -22,6 +22,12 @@
 //                        per column block.  The only cross-lane traffic per tile is a
 //                        permlane16/32 swap max-reduction.  Every KV byte is read once per
 //                        (KV head, head chunk) and shared by all query heads of the chunk.
+//   pa_partition_queue_kernel  the same work items on a work queue: as many workgroups as the
+//                        device holds at once, each building the call's item map (largest items
+//                        first) from the context lengths and taking items from a ticket counter
+//                        until none is left.  Only items with tokens are scheduled.
+//   The last workgroup to finish a split sequence's partitions merges them in the same launch
+//   (fused form), or
 //   pa_reduce_kernel     deterministic fixed-order merge of the per-partition (max, sum, acc)
 //                        records.  Skipped for sequences that fit in one partition (the
 //                        partition kernel then writes the normalised output itself) and not

@@ -316,6 +316,31 @@ def test_promotion_records_are_schema_valid_signed_and_consistent():
         assert all(case["runtime_ok"] and case["finite"] for case in record["correctness"]["cases"])
 
 
+def test_every_promoting_evaluation_is_published():
+    """An evaluation whose promotion gates all pass for the built pack has its evidence and pack-index
+    records in the tree.  The build publishes whatever promotes, so a missing record means the
+    evaluation was installed without publishing (or a stale one withdrew the records)."""
+
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("rk_publish_gates", PACKAGE / "promotion" / "publish.py")
+    publish = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(publish)
+    evidence_ids = {json.loads(p.read_text())["evidence_id"] for p in _records("evidence")}
+    checked = 0
+    for path in sorted((PACKAGE / "evaluations").glob("*-gfx950.json")):
+        operator = json.loads(path.read_text())["operator"]
+        proposal = publish.proposal_for(operator, path)
+        if proposal["recommended_decision"] != "promote":
+            continue
+        checked += 1
+        assert (PACKAGE / "pack-index" / f"{operator}-1.0.json").is_file(), operator
+        assert proposal["public_evidence"]["evidence_id"] in evidence_ids, operator
+        assert {record["evidence_id"] for record in proposal["entry_evidence"]} <= evidence_ids, operator
+    if not checked:
+        pytest.skip("no committed evaluation promotes this build")
+
+
 def test_pack_index_records_name_this_pack_and_its_release_archive():
     records = _records("pack-index")
     if not records:

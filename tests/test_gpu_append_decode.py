@@ -17,7 +17,8 @@ from _helpers import announce, make_case, to_device
 
 pytestmark = pytest.mark.gpu
 
-WORKLOAD_PARTITIONS = {"c1": 128, "c2": 256, "c3": 512, "c4": 128, "c5": 2048}
+# The dispatch entries' partition sizes (b128: 8192 tokens, slices of 512 table entries).
+WORKLOAD_PARTITIONS = {"c1": 128, "c2": 256, "c3": 512, "c4": 128, "c5": 8192}
 
 
 def new_token_slots(torch, block_tables, context_lengths, block_size):

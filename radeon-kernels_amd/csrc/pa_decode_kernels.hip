@@ -443,11 +443,17 @@ __global__ __launch_bounds__(kThreads) void pa_reduce_kernel(Params p) {
 // in how they hand out work items.  at_epilogue() runs in every wave once the item's loads have all
 // landed, at the start of its epilogue (not for an item that ends early: an empty context or a
 // partition past it); memory operations it issues are waited for only where their results are used.
-template <class E, int D, int GC, bool QK_MFMA, bool PV_MFMA, bool UB, bool AP, class Epilogue>
+template <class E, int D, int GC, bool QK_MFMA, bool PV_MFMA, bool UB, bool AP, int KVP, class Epilogue>
 __device__ __attribute__((always_inline)) inline void partition_item(const Params& p, const int tid, int b, int hslot,
                                                                      int part, const int P, Epilogue&& at_epilogue) {
   static_assert(!AP || QK_MFMA, "append-and-decode is built for the MFMA variants");
   static_assert(!PV_MFMA || QK_MFMA, "PV on MFMA takes its A operand from the QK^T MFMA's score layout");
+  static_assert(KVP == 1 || KVP == 2, "one or two KV heads per workgroup");
+  // KVP KV heads per workgroup, each run by its own group of kWaves waves exactly as a one-head
+  // workgroup runs it (same tiles, same merge order, so the same bits); the groups share the
+  // partition's block-table slice.
+  constexpr int NWAVES = kWaves * KVP;
+  constexpr int NTHREADS = kThreads * KVP;
   constexpr int KSTEPS = D / 32;       // MFMA k-steps; also DMA instructions per K tile
   constexpr int VEC = D / 16;          // elements of a token row per lane (row = 16 lanes)
   constexpr int VW = VEC / 2;          // 32-bit words per lane per token row
@@ -473,26 +479,29 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   // The K staging slots and, after the main loop, the per-wave partial accumulators share one
   // LDS buffer (a barrier separates the two uses).
   constexpr int SLOT_BYTES = KTILE16 * 16;
-  constexpr int K_STAGE_BYTES = QK_MFMA ? kWaves * SLOTS * SLOT_BYTES : 0;
-  constexpr int ACC_BYTES = kWaves * GC * D * 4;
+  constexpr int K_STAGE_BYTES = QK_MFMA ? NWAVES * SLOTS * SLOT_BYTES : 0;
+  constexpr int ACC_BYTES = NWAVES * GC * D * 4;
   constexpr int RAW_BYTES = K_STAGE_BYTES > ACC_BYTES ? K_STAGE_BYTES : ACC_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char s_raw[RAW_BYTES];
   __shared__ int s_table[kMaxSliceBlocks];
-  __shared__ float s_m[kWaves][GC];
-  __shared__ float s_l[kWaves][GC];
+  __shared__ float s_m[NWAVES][GC];
+  __shared__ float s_l[NWAVES][GC];
   __shared__ int s_last;
 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wl = wave % kWaves;    // wave within its KV head's group
+  const int kvsub = wave / kWaves;  // which of the workgroup's KV heads
   const int lane = tid & 63;
   const int g = lane >> 4;   // lane group: owns tokens 4g..4g+3 of every tile (V / scores)
   const int j = lane & 15;   // lane in group: token j of the tile for K (MFMA), V column block
   u32x4* const s_k = reinterpret_cast<u32x4*>(s_raw) + wave * SLOTS * KTILE16;
   float(*const s_acc)[GC][D] = reinterpret_cast<float(*)[GC][D]>(s_raw);
 
-  const int heads_per_seq = p.kv_heads * p.head_chunks;
-  const int kvh = hslot / p.head_chunks;
+  const int heads_per_seq = (p.kv_heads / KVP) * p.head_chunks;  // work items per (sequence, partition)
+  const int kvh0 = (hslot / p.head_chunks) * KVP;                // the workgroup's first KV head
+  const int kvh = kvh0 + kvsub;                                   // this wave's KV head
   const int chunk = hslot % p.head_chunks;
-  const int head0 = kvh * p.group + chunk * GC;  // first query head of this chunk
+  const int head0 = kvh * p.group + chunk * GC;  // first query head of this wave's chunk
   const int heads_here = min(GC, p.group - chunk * GC);
 
   // Prologue.  Every load that does not depend on the context length -- the context length
@@ -509,20 +518,20 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   const int64_t table_row = static_cast<int64_t>(b) * p.max_blocks + blk0;
   const bool is64 = p.index_is64 != 0;
   const RawIndex ctx_raw = load_raw_index(p.context_lengths, b, is64);
-  static_assert(2 * kThreads >= kMaxSliceBlocks, "two table entries per thread cover a partition's slice");
-  RawIndex ids[2] = {{~0u, ~0u}, {~0u, ~0u}};  // entries tid and tid + kThreads (a slice has <= 512)
+  static_assert(2 * NTHREADS >= kMaxSliceBlocks, "two table entries per thread cover a partition's slice");
+  RawIndex ids[2] = {{~0u, ~0u}, {~0u, ~0u}};  // entries tid and tid + NTHREADS (a slice has <= 512)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int idx = tid + i * kThreads;
+    const int idx = tid + i * NTHREADS;
     if (idx < slice) ids[i] = load_raw_index(p.block_tables, table_row + idx, is64);
   }
 
-  // Append: wave 0 lanes [0, CPR) hold one 16-byte chunk of the new token's K row of this KV head,
+  // Append: lanes [0, CPR) of each KV head's first wave hold one 16-byte chunk of the new token's K row,
   // lanes [CPR, 2 CPR) of its V row, loaded with the prologue.
   const int64_t new_row = (static_cast<int64_t>(b) * p.kv_heads + kvh) * D;
   u32x4 ap_chunk = {0u, 0u, 0u, 0u};
   if constexpr (AP) {
-    if (wave == 0 && lane < 2 * CPR) {
+    if (wl == 0 && lane < 2 * CPR) {
       const uint16_t* src = (lane < CPR ? p.new_k : p.new_v) + new_row + (lane % CPR) * 8;
       ap_chunk = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
     }
@@ -555,13 +564,13 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
     }
   }
 
-  // Block ids of this wave's first DEPTH tiles (tokens p0 + 16 * wave + 64 * n), read straight from
+  // Block ids of this wave's first DEPTH tiles (tokens p0 + 16 * wl + 64 * n), read straight from
   // the table so they can be issued before the staged slice is visible to the wave.
   RawIndex first_raw[DEPTH];
 #pragma unroll
   for (int n = 0; n < DEPTH; ++n) {
     first_raw[n] = RawIndex{~0u, ~0u};
-    const int idx = ((p0 + wave * kTile + n * kWaves * kTile) >> lb) - blk0;
+    const int idx = ((p0 + wl * kTile + n * kWaves * kTile) >> lb) - blk0;
     if (UB && idx < slice) first_raw[n] = load_raw_index(p.block_tables, table_row + idx, is64);
   }
   auto valid_block = [&](RawIndex r) -> int {
@@ -575,10 +584,12 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   if (ctx <= 0) {
     // Softmax over an empty set: NaN, as the fallback produces.  Partition 0 owns the output.
     if (part == 0) {
-      for (int idx = tid; idx < heads_here * D; idx += kThreads) {
-        const int h = idx / D, d = idx % D;
-        p.out[(static_cast<int64_t>(b) * p.query_heads + head0 + h) * D + d] =
-            E::store(__builtin_nanf(""));
+      for (int idx = tid; idx < KVP * heads_here * D; idx += NTHREADS) {
+        const int kv = KVP == 1 ? 0 : idx / (heads_here * D);
+        const int hd = KVP == 1 ? idx : idx - kv * heads_here * D;
+        const int h = hd / D, d = hd % D;
+        const int head = (kvh0 + kv) * p.group + chunk * GC + h;
+        p.out[(static_cast<int64_t>(b) * p.query_heads + head) * D + d] = E::store(__builtin_nanf(""));
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -601,7 +612,7 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   const int nblk = ((p_end - 1) >> lb) - blk0 + 1;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int idx = tid + i * kThreads;
+    const int idx = tid + i * NTHREADS;
     if (idx < nblk) s_table[idx] = valid_block(ids[i]);
   }
 
@@ -953,7 +964,7 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   // Tiles of this wave: t0 = first + n * step_tokens, n < n_tiles; tile n uses slot n % SLOTS.  The
   // loop is peeled so that every load it issues is unconditional.
   const int step_tokens = kWaves * kTile;
-  const int first = p0 + wave * kTile;
+  const int first = p0 + wl * kTile;
   const int n_tiles = first < p_end ? (p_end - first + step_tokens - 1) / step_tokens : 0;
   auto t0_of = [&](int n) { return first + n * step_tokens; };
   constexpr Flag<true> kIssue{};
@@ -978,7 +989,7 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
     // The new token's rows into its cache slot (skipped, like the append operator, when its block id
     // is invalid).  Fire and forget: no wave of this launch reads the slot, and the explicit memory
     // waits below stay exact (a store issued before a tile's loads only makes them wait longer).
-    if (ap_here && chunk == 0 && wave == 0 && lane < 2 * CPR) {
+    if (ap_here && chunk == 0 && wl == 0 && lane < 2 * CPR) {
       const int pb = s_table[(ap_pos >> lb) - blk0];
       if (pb >= 0) {
         uint16_t* dst = (lane < CPR ? p.k_store : p.v_store) + static_cast<int64_t>(pb) * p.block_stride +
@@ -1061,22 +1072,26 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   }
   __syncthreads();
 
-  // Merge the four waves (fixed order) and emit either the final output or a partition record.
+  // Merge each KV head's four waves (fixed order) and emit either the final output or a partition
+  // record.
   const bool single = (np == 1);
-  for (int idx = tid; idx < heads_here * D; idx += kThreads) {
-    const int h = idx / D, d = idx % D;
+  for (int idx = tid; idx < KVP * heads_here * D; idx += NTHREADS) {
+    const int kv = KVP == 1 ? 0 : idx / (heads_here * D);
+    const int hd = KVP == 1 ? idx : idx - kv * heads_here * D;
+    const int h = hd / D, d = hd % D;
+    const int w0 = kv * kWaves;
     float M = neg_inf;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w0 + w][h]);
     float L = 0.0f, A = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float mw = s_m[w][h];
+      const float mw = s_m[w0 + w][h];
       const float f = (mw == neg_inf) ? 0.0f : fast_exp2(mw - M);
-      L = fmaf(s_l[w][h], f, L);
-      A = fmaf(s_acc[w][h][d], f, A);
+      L = fmaf(s_l[w0 + w][h], f, L);
+      A = fmaf(s_acc[w0 + w][h][d], f, A);
     }
-    const int64_t row = q_row0 + h;
+    const int64_t row = static_cast<int64_t>(b) * p.query_heads + (kvh0 + kv) * p.group + chunk * GC + h;
     if (single) {
       p.out[row * D + d] = E::store(A / L);
     } else {
@@ -1107,7 +1122,12 @@ __device__ __attribute__((always_inline)) inline void partition_item(const Param
   }
   __syncthreads();
   if (s_last == 0) return;
-  for (int h = wave; h < heads_here; h += kWaves) merge_partitions<E, D, true>(p, q_row0 + h, np, lane);
+  for (int r = wave; r < KVP * heads_here; r += NWAVES) {
+    const int kv = KVP == 1 ? 0 : r / heads_here;
+    const int h = KVP == 1 ? r : r - kv * heads_here;
+    const int64_t row = static_cast<int64_t>(b) * p.query_heads + (kvh0 + kv) * p.group + chunk * GC + h;
+    merge_partitions<E, D, true>(p, row, np, lane);
+  }
 }
 
 // Grid schedule: one workgroup per work item, every item of the batch x head slots x partitions
@@ -1126,7 +1146,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(Params p) {
   const int64_t rest = wg / heads_per_seq;
   const int b = static_cast<int>(rest % p.batch);
   const int part = static_cast<int>(rest / p.batch);
-  partition_item<E, D, GC, QK_MFMA, PV_MFMA, UB, AP>(p, static_cast<int>(threadIdx.x), b, hslot, part, p.partition_tokens,
+  partition_item<E, D, GC, QK_MFMA, PV_MFMA, UB, AP, 1>(p, static_cast<int>(threadIdx.x), b, hslot, part, p.partition_tokens,
                                             [] {});
 }
 
@@ -1165,14 +1185,14 @@ __device__ __forceinline__ void descending_offsets(int* s_count, int lane) {
 // once the bins hold the descending offsets (s_count[v] = sequences with a larger key).  The
 // sequences are placed in rounds of one per thread, in index order: a sequence's position is its
 // key's offset, plus the sequences of that key placed in earlier rounds, plus those of lower thread
-// index in this round.  O(batch) work per thread for the histogram and at most 256 key compares
-// per round, against the O(batch) compares per sequence of a plain rank.
-template <class Key, class Hook>
+// index in this round.  O(batch) work per thread for the histogram and at most NT (the workgroup's
+// threads) key compares per round, against the O(batch) compares per sequence of a plain rank.
+template <int NT, class Key, class Hook>
 __device__ __attribute__((always_inline)) inline int queue_sort(int batch, int tid, Key&& key, uint16_t* order,
                                                                 int* s_count, int16_t* s_round, Hook&& before_rounds) {
-  for (int v = tid; v < kQueueBins; v += kThreads) s_count[v] = 0;
+  for (int v = tid; v < kQueueBins; v += NT) s_count[v] = 0;
   __syncthreads();
-  for (int i = tid; i < batch; i += kThreads) {
+  for (int i = tid; i < batch; i += NT) {
     const int k = key(i);
     if (k >= 0) atomicAdd(&s_count[k], 1);
   }
@@ -1182,7 +1202,7 @@ __device__ __attribute__((always_inline)) inline int queue_sort(int batch, int t
   before_rounds(s_count);
   __syncthreads();
   int placed = 0;
-  for (int base = 0; base < batch; base += kThreads) {
+  for (int base = 0; base < batch; base += NT) {
     const int i = base + tid;
     const int k = i < batch ? key(i) : -1;
     s_round[tid] = static_cast<int16_t>(k);
@@ -1232,32 +1252,34 @@ __device__ __attribute__((always_inline)) inline int queue_sort(int batch, int t
 // measured 3% slower on the 128-sequence ragged workload; this order of items measured 1.5%
 // faster than partition-major levels over all partitions.  The counter only grows, so every
 // workgroup exits after at most items / gridDim.x + 1 tickets.
-template <class E, int D, int GC, bool PV_MFMA, bool UB, bool AP>
-__global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) {
+template <class E, int D, int GC, bool PV_MFMA, bool UB, bool AP, int KVP>
+__global__ __launch_bounds__(kThreads * KVP) void pa_partition_queue_kernel(Params p) {
+  constexpr int NTHREADS = kThreads * KVP;
   __shared__ uint16_t s_full[kQueueMaxBatch];        // full partitions of sequence b
   __shared__ int16_t s_class[kQueueMaxBatch];        // size class of its partial partition, -1: none
   __shared__ uint16_t s_full_order[kQueueMaxBatch];  // sequences by full count, descending
   __shared__ uint16_t s_part_order[kQueueMaxBatch];  // sequences with a partial, by size class, descending
   __shared__ int s_level[kQueueMaxLevels + 1];       // first item of each full level; [levels] = full items
   __shared__ int s_count[kQueueBins];
-  __shared__ __attribute__((aligned(16))) int16_t s_round[kThreads];
+  __shared__ __attribute__((aligned(16))) int16_t s_round[NTHREADS];
   __shared__ int s_levels;
   __shared__ int s_partials;
   __shared__ int s_next[2][4];  // ticket, sequence, head slot, partition; by item parity
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int heads_per_seq = p.kv_heads * p.head_chunks;
+  const int heads_per_seq = (p.kv_heads / KVP) * p.head_chunks;  // work items per (sequence, partition)
   const bool is64 = p.index_is64 != 0;
   const int64_t max_ctx = static_cast<int64_t>(p.max_blocks) << p.bs_log2;
   __shared__ unsigned long long s_tokens;
 
-  // This thread's sequences (tid + r * kThreads; the host admits at most kQueueMaxBatch) and their
+  // This thread's sequences (tid + r * NTHREADS; the host admits at most kQueueMaxBatch) and their
   // context lengths clamped to the table, loaded once for the partition size and the item map.
-  constexpr int kSeqPerThread = kQueueMaxBatch / kThreads;
+  static_assert(kQueueMaxBatch % NTHREADS == 0, "sequences split evenly over the threads");
+  constexpr int kSeqPerThread = kQueueMaxBatch / NTHREADS;
   int cc_own[kSeqPerThread];
 #pragma unroll
   for (int r = 0; r < kSeqPerThread; ++r) {
-    const int i = tid + r * kThreads;
+    const int i = tid + r * NTHREADS;
     cc_own[r] = 0;
     if (i < p.batch) {
       const int64_t c = index_value(load_raw_index(p.context_lengths, i, is64), is64);
@@ -1298,7 +1320,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
   }
 #pragma unroll
   for (int r = 0; r < kSeqPerThread; ++r) {
-    const int i = tid + r * kThreads;
+    const int i = tid + r * NTHREADS;
     if (i < p.batch) {
       const int cc = cc_own[r];
       const int rem = cc <= 0 ? 0 : cc % P;
@@ -1309,9 +1331,9 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
   __syncthreads();
   // Full order.  Before its rounds the bins hold, for level k, the number of sequences with more than
   // k full partitions: the level's size.
-  queue_sort(p.batch, tid, [&](int i) { return static_cast<int>(s_full[i]); }, s_full_order, s_count, s_round,
-             [&](const int* count) {
-               for (int v = tid; v < kQueueMaxLevels; v += kThreads) {
+  queue_sort<NTHREADS>(p.batch, tid, [&](int i) { return static_cast<int>(s_full[i]); }, s_full_order, s_count,
+                       s_round, [&](const int* count) {
+               for (int v = tid; v < kQueueMaxLevels; v += NTHREADS) {
                  s_level[v + 1] = count[v] * heads_per_seq;
                  if (count[v] > 0) atomicMax(&s_levels, v + 1);
                }
@@ -1343,8 +1365,8 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
     if (lane == 0) s_level[0] = 0;
   }
   // Partial order (its bins are free again: the full order's rounds are done).
-  const int placed = queue_sort(p.batch, tid, [&](int i) { return static_cast<int>(s_class[i]); }, s_part_order,
-                                s_count, s_round, [](const int*) {});
+  const int placed = queue_sort<NTHREADS>(p.batch, tid, [&](int i) { return static_cast<int>(s_class[i]); },
+                                          s_part_order, s_count, s_round, [](const int*) {});
   if (placed > 0) atomicAdd(&s_partials, placed);
   __syncthreads();
   const int full_items = __builtin_amdgcn_readfirstlane(s_level[levels]);
@@ -1398,7 +1420,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_queue_kernel(Params p) 
     // through every item's epilogue (hoisted, they took the 128-dim GQA-4 form to one wave per SIMD).
     int item_tid = tid;
     __asm__ volatile("" : "+v"(item_tid));
-    partition_item<E, D, GC, true, PV_MFMA, UB, AP>(p, item_tid, b, hslot, part, P, [&]() __attribute__((always_inline)) {
+    partition_item<E, D, GC, true, PV_MFMA, UB, AP, KVP>(p, item_tid, b, hslot, part, P, [&]() __attribute__((always_inline)) {
       if (tid == 0) {
         claimed = ticket();
         has_claim = true;
@@ -1438,13 +1460,13 @@ struct Residency {
   hipError_t err;
   int per_cu;
 };
-template <class E, int D, int GC, bool PV_MFMA, bool UB, bool AP>
+template <class E, int D, int GC, bool PV_MFMA, bool UB, bool AP, int KVP>
 hipError_t queue_capacity(int64_t* capacity) {
   static const Residency r = [] {
     Residency out{hipSuccess, 0};
     out.err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &out.per_cu, reinterpret_cast<const void*>(&pa_partition_queue_kernel<E, D, GC, PV_MFMA, UB, AP>), kThreads,
-        0);
+        &out.per_cu, reinterpret_cast<const void*>(&pa_partition_queue_kernel<E, D, GC, PV_MFMA, UB, AP, KVP>),
+        kThreads * KVP, 0);
     return out;
   }();
   if (r.err != hipSuccess) return r.err;
@@ -1463,17 +1485,55 @@ hipError_t queue_capacity(int64_t* capacity) {
   return hipSuccess;
 }
 
-// The partition launch for `items` work items.  For a queue-eligible call (a split-K shape whose
-// item map fits the queue kernel; prm.queue is then its ticket counter) the work-queue schedule runs
-// when asked for, or, by default, when the items exceed what the device holds at once and partitions
-// hold at least kQueueMinPartitionTokens tokens; otherwise one workgroup per item.  With `chosen`, nothing is launched: the schedule is stored there instead.
+// KV-head pairs.  The work queue can run two KV heads per workgroup (8 waves, four per KV head).  At
+// head_dim 128 a token's row of one KV head is 256 bytes and the two heads' rows are adjacent; the
+// workgroup's two wave groups read them at nearly the same time.  A read-only probe of the
+// 128-sequence ragged access pattern streamed 7.0 TB/s that way against 6.5 TB/s with one head per
+// workgroup, at equal workgroups, bytes and loads in flight.  Every KV head runs exactly as in a
+// one-head workgroup, so the outputs do not change.
+//
+// The pairs hold a CU's one 8-wave workgroup in step: an item's prologue and epilogue no longer
+// overlap another workgroup's streaming on the same CU, and the CU's share of the call's tail is
+// coarser.  They pay on long calls of long items and lose on short ones, so they run only with head
+// chunks of at most 4 (8-head chunks measured 0.5-8% slower), without partition growth, with
+// partitions of at least kPairMinPartitionTokens and at least kPairMinRows (sequence, KV head)
+// rows.  Measured against one head per workgroup (head_dim 128, fused): 128 sequences of 1k-16k
+// tokens, GQA 32x8, P 8192 -2.0% and P 4096 -1.7%; 32 sequences at P 4096 +4.5%; 64 sequences
+// with growth +2.1%; 512 sequences with growth -0.9%.
+template <int D, int GC, bool PV_MFMA, bool UB>
+constexpr bool kPairsKvHeads = D == 128 && GC <= 4 && PV_MFMA && UB;
+constexpr int kPairMinPartitionTokens = 4096;
+constexpr int64_t kPairMinRows = 1024;
+__device__ __host__ constexpr bool pair_kv_heads(int kv_heads, int batch, int partition_tokens, int grow_max_tokens) {
+  return kv_heads % 2 == 0 && grow_max_tokens <= partition_tokens && partition_tokens >= kPairMinPartitionTokens &&
+         static_cast<int64_t>(batch) * kv_heads >= kPairMinRows;
+}
+
+template <class E, int D, int GC, bool PV_MFMA, bool UB, bool AP, int KVP>
+hipError_t launch_queue_kernel(const Params& prm, int64_t items, hipStream_t stream) {
+  int64_t capacity = 0;
+  const hipError_t err = queue_capacity<E, D, GC, PV_MFMA, UB, AP, KVP>(&capacity);
+  if (err != hipSuccess) return err;
+  const int64_t own = items / KVP;  // this kernel's work items (KVP KV heads each)
+  const int64_t grid = own < capacity ? own : capacity;
+  hipLaunchKernelGGL((pa_partition_queue_kernel<E, D, GC, PV_MFMA, UB, AP, KVP>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(kThreads * KVP), 0, stream, prm);
+  return hipGetLastError();
+}
+
+// The partition launch for `items` work items (one KV head each).  For a queue-eligible call (a
+// split-K shape whose item map fits the queue kernel; prm.queue is then its ticket counter) the
+// work-queue schedule runs when asked for, or, by default, when the items exceed what the device
+// holds at once of the one-head queue kernel and partitions hold at least kQueueMinPartitionTokens
+// tokens; otherwise one workgroup per item.  With `chosen`, nothing is launched: the schedule is
+// stored there instead.
 template <class E, int D, int GC, bool QK_MFMA, bool PV_MFMA, bool UB, bool AP>
 hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedule, bool queue_ok, hipStream_t stream,
                                    int* chosen) {
   if constexpr (QK_MFMA) {
     if (queue_ok) {
       int64_t capacity = 0;
-      const hipError_t err = queue_capacity<E, D, GC, PV_MFMA, UB, AP>(&capacity);
+      const hipError_t err = queue_capacity<E, D, GC, PV_MFMA, UB, AP, 1>(&capacity);
       if (err != hipSuccess) return err;
       if (schedule == kScheduleQueue ||
           (schedule == kScheduleAuto && items > capacity && prm.partition_tokens >= kQueueMinPartitionTokens)) {
@@ -1483,10 +1543,11 @@ hipError_t launch_partition_kernel(const Params& prm, int64_t items, int schedul
         }
         if (prm.queue_done == nullptr)
           hipLaunchKernelGGL(pa_queue_reset_kernel, dim3(1), dim3(kWave), 0, stream, prm.queue);
-        const int64_t grid = items < capacity ? items : capacity;
-        hipLaunchKernelGGL((pa_partition_queue_kernel<E, D, GC, PV_MFMA, UB, AP>), dim3(static_cast<uint32_t>(grid)),
-                           dim3(kThreads), 0, stream, prm);
-        return hipGetLastError();
+        if constexpr (kPairsKvHeads<D, GC, PV_MFMA, UB>) {
+          if (pair_kv_heads(prm.kv_heads, prm.batch, prm.partition_tokens, prm.grow_max_tokens))
+            return launch_queue_kernel<E, D, GC, PV_MFMA, UB, AP, 2>(prm, items, stream);
+        }
+        return launch_queue_kernel<E, D, GC, PV_MFMA, UB, AP, 1>(prm, items, stream);
       }
     }
   }

@@ -7,7 +7,8 @@ The cases cover what the queue's item map is built from: ragged contexts whose p
 differ per sequence, empty and negative contexts (one NaN item), contexts past the table, int32 and
 int64 indices, head chunks of 1, 2 and 4 query heads (and two chunks per KV head), block sizes below
 a tile, every head_dim, the fused, two-launch, phase-split, append and allocation-free entries, a
-garbage-filled workspace header, repeated calls and a smaller call after a larger one.
+garbage-filled workspace header, repeated calls and a smaller call after a larger one, and the
+128-sequence ragged workload, on which the queue runs two KV heads per workgroup.
 """
 
 from __future__ import annotations
@@ -253,3 +254,31 @@ def test_queue_under_graph_capture_replays_match_eager(gpu, palib):
         torch.cuda.synchronize()
         assert same_bits(captured, eager)
         del scratch
+
+
+@pytest.mark.parametrize("partition", [8192, 4096])
+def test_kv_head_pairs_match_the_grid(gpu, palib, c5_case, partition):
+    """The 128-sequence ragged workload at partitions of at least 4096 tokens: 1024 (sequence, KV head)
+    rows and head chunks of 4, so the work queue runs two KV heads per 8-wave workgroup.  Each KV head
+    runs as in a one-head workgroup, so every form must match the one-head grid bit for bit: fused,
+    two-launch and allocation-free; and the float64 oracle within the bf16 bar."""
+
+    import torch
+
+    data = c5_case["gpu"]
+    args = [data[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    batch, query_heads, head_dim = (int(s) for s in data["query"].shape)
+    _, block_size, kv_heads, _ = (int(s) for s in data["key_cache"].shape)
+    max_blocks = int(data["block_tables"].shape[1])
+    assert batch * kv_heads >= 1024
+    assert palib.schedule(batch, query_heads, kv_heads, head_dim, block_size, max_blocks, "bf16", partition) == "queue"
+    announce(f"c5 KV-head pairs, partition {partition}")
+    grid = palib.decode(*args, partition_tokens=partition, phase="fused", schedule="grid")
+    fused = palib.decode(*args, partition_tokens=partition, phase="fused")
+    two_launch = palib.decode(*args, partition_tokens=partition)
+    out = torch.empty_like(data["query"])
+    noalloc = palib.decode_noalloc(*args, out=out, partition_tokens=partition)
+    torch.cuda.synchronize()
+    for name, got in (("fused", fused), ("two-launch", two_launch), ("allocation-free", noalloc)):
+        assert same_bits(got, grid), f"{name} work queue differs from the grid at partition {partition}"
+    assert_within(fused.cpu(), c5_case["expected"], "bf16", f"c5 pairs P{partition}")

@@ -25,7 +25,9 @@
 //   pa_partition_queue_kernel  the same work items on a work queue: as many workgroups as the
 //                        device holds at once, each building the call's item map (largest items
 //                        first) from the context lengths and taking items from a ticket counter
-//                        until none is left.  Only items with tokens are scheduled.
+//                        until none is left.  Only items with tokens are scheduled.  On long GQA
+//                        calls at head_dim 128 (pair_kv_heads) one 8-wave workgroup runs two
+//                        adjacent KV heads of an item, four waves each, with the same bits.
 //   The last workgroup to finish a split sequence's partitions merges them in the same launch
 //   (fused form), or
 //   pa_reduce_kernel     deterministic fixed-order merge of the per-partition (max, sum, acc)

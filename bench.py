@@ -112,7 +112,7 @@ PUBLIC_CALLS_MIN = 200
 def public_call_us(torch, call, steps: int, batches: int = 5) -> float:
     """Host wall time per call of the public operator: the median of ``batches`` batches of ``steps``
     (at least PUBLIC_CALLS_MIN) back-to-back calls, each batch closed by a synchronisation (single
-    batches were seen to catch one-off host stalls of the box; batches of 10 calls added the two
+    batches were seen to catch one-off host stalls of the machine; batches of 10 calls added the two
     synchronisations, 2-3 us, to every microsecond-scale call)."""
 
     import statistics
@@ -834,7 +834,7 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            # The committed rocprofv3 summary of this configuration (another run, usually another box):
+            # The committed rocprofv3 summary of this configuration (another run, usually another machine):
             # its kernel-trace average and the fraction of peak that average gives.
             "profile": None if summary is None or summary[2] is None else {
                 "summary": str(summary[0].relative_to(ROOT)), "kernel_avg_us": summary[2],

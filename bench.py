@@ -6,10 +6,11 @@ the workload's dispatch entry selects (launch.merge): "reduce" -- the partition 
 partition-reduce kernel -- or "fused" -- the partition kernel alone, its last workgroup per sequence
 and head slot merging the partition records.  --merge overrides the entry.  The library runs the
 partition kernel on the work-queue schedule when the call's work items exceed the workgroups the GPU
-holds at once (config.schedule; the kernel is then pa_partition_queue_kernel, launched behind a
-one-thread kernel that zeroes its ticket counter), else one workgroup per work item.  Default workload: 128 sequences, 32 query / 8 KV heads, head_dim
-128, block 16, bf16, context lengths ~ U[1024, 16384] (seeded), about 4.8 GB of K/V per call -- 18x
-the 256 MB last-level cache, so every call streams from HBM.
+holds at once (config.schedule; the kernel is then pa_partition_queue_kernel, whose ticket counter
+resets itself in the fused form and is zeroed by a one-thread kernel in front of it in the reduce
+form), else one workgroup per work item.  Default workload: 128 sequences, 32 query / 8 KV heads,
+head_dim 128, block 16, bf16, context lengths ~ U[1024, 16384] (seeded), 4.24 GB of K/V per call --
+about 16x the 256 MB last-level cache, so every call streams from HBM.
 
 Timing: every form below is timed as S (--samples, default 10) interleaved samples of K (--steps)
 back-to-back launches, each sample bracketed by synchronisations and HIP events on the launch
@@ -21,8 +22,8 @@ Prints one JSON line:
   us_per_call      median wall time per call of the headline form: K whole calls back to back,
                    nothing else on the stream (us_per_call_events: the same samples by HIP events)
   roofline         the partition kernel against the 8 TB/s HBM peak: achieved = KV bytes / its
-                   median duration by HIP events (in the fused form the call is that one kernel,
-                   plus the queue's counter reset on the work-queue schedule); traffic = measured
+                   median duration by HIP events (in the fused form the call is that one kernel);
+                   traffic = measured
                    HBM bytes per launch from the committed rocprofv3 counter summary for this exact
                    configuration (null when there is none)
   kernels_us       per-launch averages of the reduce form's two kernels; us_per_call_reduce and

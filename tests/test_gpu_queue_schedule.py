@@ -7,8 +7,9 @@ The cases cover what the queue's item map is built from: ragged contexts whose p
 differ per sequence, empty and negative contexts (one NaN item), contexts past the table, int32 and
 int64 indices, head chunks of 1, 2 and 4 query heads (and two chunks per KV head), block sizes below
 a tile, every head_dim, the fused, two-launch, phase-split, append and allocation-free entries, a
-garbage-filled workspace header, repeated calls and a smaller call after a larger one, and the
-128-sequence ragged workload, on which the queue runs two KV heads per workgroup.
+garbage-filled workspace header, repeated calls and a smaller call after a larger one, and the calls
+on which the queue runs two KV heads per workgroup: the 128-sequence ragged workload and four other
+layouts (head chunks of 4, 2 and 1, blocks of 16 to 128 tokens, both dtypes and index types).
 """
 
 from __future__ import annotations
@@ -282,3 +283,43 @@ def test_kv_head_pairs_match_the_grid(gpu, palib, c5_case, partition):
     for name, got in (("fused", fused), ("two-launch", two_launch), ("allocation-free", noalloc)):
         assert same_bits(got, grid), f"{name} work queue differs from the grid at partition {partition}"
     assert_within(fused.cpu(), c5_case["expected"], "bf16", f"c5 pairs P{partition}")
+
+
+# (query_heads, kv_heads, block_size, dtype, index_dtype, batch): layouts the work queue pairs KV heads
+# on besides the 128-sequence workload: head chunks of 4, 2 and 1, blocks of 16 to 128 tokens, both
+# dtypes and index types, and 16 KV heads.
+PAIR_LAYOUTS = [
+    (32, 8, 64, "fp16", "int64", 128),
+    (16, 8, 128, "bf16", "int32", 128),
+    (8, 8, 32, "bf16", "int64", 128),
+    (16, 16, 16, "fp16", "int32", 64),
+]
+
+
+@pytest.mark.parametrize("layout", PAIR_LAYOUTS, ids=lambda s: f"h{s[0]}x{s[1]}-bs{s[2]}-{s[3]}-{s[4]}-b{s[5]}")
+def test_kv_head_pairs_on_other_layouts(gpu, palib, layout):
+    """At least 1024 (sequence, KV head) rows at partitions of 4096 tokens: the work queue runs two KV
+    heads per 8-wave workgroup.  Ragged contexts (one and two partitions, empty, negative and past the
+    table) must match the one-head grid bit for bit, fused and two-launch, and the float64 oracle on
+    sampled sequences (the edge ones included)."""
+
+    import torch
+
+    hq, hkv, bs, dtype, index, batch = layout
+    limit, partition = 8192, 4096
+    assert batch * hkv >= 1024 and hkv % 2 == 0 and hq // hkv <= 4
+    contexts = ragged_contexts(batch, limit, seed=bs + hq)
+    case = make_case(torch, batch=batch, query_heads=hq, kv_heads=hkv, head_dim=128, block_size=bs,
+                     contexts=contexts, max_blocks=limit // bs, dtype=dtype, index_dtype=index, seed=hkv + bs)
+    dev = to_device(case, gpu)
+    args = [dev[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    assert palib.schedule(batch, hq, hkv, 128, bs, limit // bs, dtype, partition) == "queue"
+    announce(f"KV-head pairs h{hq}x{hkv} bs{bs} {dtype} {index} batch {batch}")
+    grid = palib.decode(*args, partition_tokens=partition, phase="fused", schedule="grid")
+    fused = palib.decode(*args, partition_tokens=partition, phase="fused")
+    two_launch = palib.decode(*args, partition_tokens=partition)
+    torch.cuda.synchronize()
+    assert same_bits(fused, grid)
+    assert same_bits(two_launch, grid)
+    sampled = sorted({0, 1, 2, 3, batch // 2, batch // 2 + 1, batch - 3, batch - 2, batch - 1})
+    assert_within(fused[sampled].cpu(), oracle64(case, sequences=sampled), dtype, f"pairs h{hq}x{hkv} bs{bs}")

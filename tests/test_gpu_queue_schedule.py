@@ -323,3 +323,37 @@ def test_kv_head_pairs_on_other_layouts(gpu, palib, layout):
     assert same_bits(two_launch, grid)
     sampled = sorted({0, 1, 2, 3, batch // 2, batch // 2 + 1, batch - 3, batch - 2, batch - 1})
     assert_within(fused[sampled].cpu(), oracle64(case, sequences=sampled), dtype, f"pairs h{hq}x{hkv} bs{bs}")
+
+
+def test_kv_head_pairs_under_graph_capture(gpu, c5_case):
+    """The public call on the 128-sequence workload (its exact dispatch entry: partitions of 8192, two KV
+    heads per work-queue workgroup) captured into a HIP graph: the capture takes the two-launch form (ticket
+    reset kernel, paired queue kernel, reduce kernel); every replay must equal the eager fused call bit for
+    bit, with unrelated eager work between replays."""
+
+    import torch
+
+    import radeon_kernels as rk
+
+    data = c5_case["gpu"]
+    args = [data[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lengths")]
+    announce("c5 KV-head pairs under graph capture")
+    eager = rk.paged_attention_decode(*args)
+    record = rk.get_last_dispatch()
+    assert int(record["launch"]["partition_tokens"]) == 8192, record["launch"]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            rk.paged_attention_decode(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = rk.paged_attention_decode(*args)
+    for _ in range(3):
+        scratch = torch.randn(1 << 20, device=gpu)  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert same_bits(captured, eager)
+        del scratch
+    del graph

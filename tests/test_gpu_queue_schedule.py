@@ -8,8 +8,9 @@ differ per sequence, empty and negative contexts (one NaN item), contexts past t
 int64 indices, head chunks of 1, 2 and 4 query heads (and two chunks per KV head), block sizes below
 a tile, every head_dim, the fused, two-launch, phase-split, append and allocation-free entries, a
 garbage-filled workspace header, repeated calls and a smaller call after a larger one, and the calls
-on which the queue runs two KV heads per workgroup: the 128-sequence ragged workload and four other
-layouts (head chunks of 4, 2 and 1, blocks of 16 to 128 tokens, both dtypes and index types).
+on which the queue runs two KV heads per workgroup: the 128-sequence ragged workload (also under graph
+capture) and six other layouts (head chunks of 4, 2 and 1, blocks of 16 to 128 tokens, both dtypes and
+index types, one to eight KV-head pairs per sequence).
 """
 
 from __future__ import annotations
@@ -285,18 +286,20 @@ def test_kv_head_pairs_match_the_grid(gpu, palib, c5_case, partition):
     assert_within(fused.cpu(), c5_case["expected"], "bf16", f"c5 pairs P{partition}")
 
 
-# (query_heads, kv_heads, block_size, dtype, index_dtype, batch): layouts the work queue pairs KV heads
-# on besides the 128-sequence workload: head chunks of 4, 2 and 1, blocks of 16 to 128 tokens, both
-# dtypes and index types, and 16 KV heads.
+# (query_heads, kv_heads, block_size, dtype, index_dtype, batch, limit): layouts the work queue pairs KV
+# heads on besides the 128-sequence workload: head chunks of 4, 2 and 1, blocks of 16 to 128 tokens, both
+# dtypes and index types, and 16, 6 (three pairs per sequence) and 2 (one pair) KV heads.
 PAIR_LAYOUTS = [
-    (32, 8, 64, "fp16", "int64", 128),
-    (16, 8, 128, "bf16", "int32", 128),
-    (8, 8, 32, "bf16", "int64", 128),
-    (16, 16, 16, "fp16", "int32", 64),
+    (32, 8, 64, "fp16", "int64", 128, 8192),
+    (16, 8, 128, "bf16", "int32", 128, 8192),
+    (8, 8, 32, "bf16", "int64", 128, 8192),
+    (16, 16, 16, "fp16", "int32", 64, 8192),
+    (24, 6, 32, "bf16", "int32", 176, 8192),
+    (8, 2, 16, "fp16", "int64", 512, 4608),
 ]
 
 
-@pytest.mark.parametrize("layout", PAIR_LAYOUTS, ids=lambda s: f"h{s[0]}x{s[1]}-bs{s[2]}-{s[3]}-{s[4]}-b{s[5]}")
+@pytest.mark.parametrize("layout", PAIR_LAYOUTS, ids=lambda s: f"h{s[0]}x{s[1]}-bs{s[2]}-{s[3]}-{s[4]}-b{s[5]}-c{s[6]}")
 def test_kv_head_pairs_on_other_layouts(gpu, palib, layout):
     """At least 1024 (sequence, KV head) rows at partitions of 4096 tokens: the work queue runs two KV
     heads per 8-wave workgroup.  Ragged contexts (one and two partitions, empty, negative and past the
@@ -305,8 +308,8 @@ def test_kv_head_pairs_on_other_layouts(gpu, palib, layout):
 
     import torch
 
-    hq, hkv, bs, dtype, index, batch = layout
-    limit, partition = 8192, 4096
+    hq, hkv, bs, dtype, index, batch, limit = layout
+    partition = 4096
     assert batch * hkv >= 1024 and hkv % 2 == 0 and hq // hkv <= 4
     contexts = ragged_contexts(batch, limit, seed=bs + hq)
     case = make_case(torch, batch=batch, query_heads=hq, kv_heads=hkv, head_dim=128, block_size=bs,

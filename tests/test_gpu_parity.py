@@ -118,6 +118,8 @@ SHAPES = [
     (32, 4, 128, 64, "bf16"),
     (8, 2, 128, 1, "fp16"),     # one token per block
     (6, 2, 64, 128, "bf16"),
+    (8, 2, 128, 256, "bf16"),   # the largest block the C ABI takes
+    (16, 16, 64, 256, "fp16"),
 ]
 
 

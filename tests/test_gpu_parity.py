@@ -120,6 +120,8 @@ SHAPES = [
     (6, 2, 64, 128, "bf16"),
     (8, 2, 128, 256, "bf16"),   # the largest block the C ABI takes
     (16, 16, 64, 256, "fp16"),
+    (32, 1, 128, 16, "fp16"),   # multi-query: one KV head, group 32 (four 8-head chunks)
+    (64, 1, 64, 32, "bf16"),    # multi-query, group 64
 ]
 
 

@@ -44,7 +44,7 @@ def ragged_contexts(batch, limit, seed):
 
 # (query_heads, kv_heads, head_dim, block_size, dtype, index_dtype, partition): head chunks of 4, 1,
 # 2 and 8 (group 8 at head_dim 256: one chunk of 8 with PV on MFMA, two chunks of 4 otherwise); blocks of
-# 16, 32, 8 and 1 tokens; every head_dim.
+# 16, 32, 8 and 1 tokens; every head_dim; and multi-query (one KV head, four 8-head chunks).
 SHAPES = [
     (32, 8, 128, 16, "bf16", "int32", 128),
     (16, 16, 64, 32, "bf16", "int64", 64),
@@ -52,6 +52,7 @@ SHAPES = [
     (64, 8, 128, 1, "bf16", "int32", 64),
     (32, 8, 256, 16, "fp16", "int32", 128),
     (64, 8, 256, 16, "bf16", "int32", 256),
+    (32, 1, 128, 16, "fp16", "int32", 128),
 ]
 
 

@@ -98,6 +98,8 @@ SHAPES = [
     (64, 8, 256, 16, "fp16"),   # group 8 at head_dim 256: one 8-head chunk (PV on MFMA)
     (4, 4, 256, 8, "fp16"),     # blocks smaller than a tile
     (8, 2, 128, 1, "fp16"),     # one token per block
+    (32, 1, 128, 16, "bf16"),   # multi-query: four 8-head chunks, the first one stores
+    (8, 2, 128, 256, "fp16"),   # the largest block the C ABI takes
 ]
 
 

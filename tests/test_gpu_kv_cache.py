@@ -9,7 +9,9 @@ contracts/kv_cache_copy-1.0.json:21).
 * append then decode: tokens written by the append are read by the decode exactly where the block
   tables put them (the two halves of a decode step, on the same cache layout);
 * block copy: every case of kv_cache_copy-1.0.yaml, both dtypes and index types, through the C ABI;
-  ``rk.kv_cache_copy`` selects the gfx950 winner; pairs with an out-of-range block are skipped.
+  ``rk.kv_cache_copy`` selects the gfx950 winner; pairs with an out-of-range block are skipped;
+* both operators on layouts beyond the reference's cases: blocks of 1 to 256 tokens, one and three KV
+  heads, head_dim 64, 96 and 256.
 """
 
 from __future__ import annotations
@@ -203,3 +205,46 @@ def test_public_copy_selects_the_gfx950_kernel_and_skips_out_of_range_pairs(gpu,
     kvlib.copy(dev["key_cache"], dev["value_cache"], dev["block_mapping"])
     torch.cuda.synchronize()
     assert_caches(dev["key_cache"], dev["value_cache"], expected, "out-of-range pairs")
+
+
+# Layouts beyond the reference's cases: one-token and 256-token blocks, one and three KV heads, head_dim
+# 64, 96 and 256 (cache rows of any multiple of 16 bytes).
+OTHER_APPEND = [
+    AppendCase("bs1-kv1-d64", 37, 64, 1, 1, 64),
+    AppendCase("bs256-kv2-d128", 50, 12, 256, 2, 128),
+    AppendCase("bs8-kv3-d96", 19, 40, 8, 3, 96),
+    AppendCase("bs128-kv1-d256", 7, 16, 128, 1, 256),
+]
+OTHER_COPY = [
+    CopyCase("bs1-kv1-d64", 5, 32, 1, 1, 64),
+    CopyCase("bs256-kv2-d128", 3, 8, 256, 2, 128),
+    CopyCase("bs8-kv3-d96", 4, 20, 8, 3, 96),
+]
+
+
+@pytest.mark.parametrize("case", OTHER_APPEND, ids=lambda c: c.key)
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_append_on_other_layouts(gpu, kvlib, case, dtype):
+    import torch
+
+    data = make_append_inputs(case, dtype=dtype, index_dtype="int32", seed=case.tokens)
+    expected = expected_bits(data)
+    dev = {k: v.to(gpu) for k, v in data.items() if hasattr(v, "to")}
+    announce(f"kv append {case.key} {dtype}")
+    kc, vc = kvlib.append(dev["key"], dev["value"], dev["key_cache"], dev["value_cache"], dev["slot_mapping"])
+    torch.cuda.synchronize()
+    assert_caches(kc, vc, expected, f"append {case.key}/{dtype}")
+
+
+@pytest.mark.parametrize("case", OTHER_COPY, ids=lambda c: c.key)
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_copy_on_other_layouts(gpu, kvlib, case, dtype):
+    import torch
+
+    data = make_copy_inputs(case, dtype=dtype, index_dtype="int64", seed=case.pairs)
+    expected = expected_copy_bits(data)
+    dev = {k: v.to(gpu) for k, v in data.items() if hasattr(v, "to")}
+    announce(f"kv copy {case.key} {dtype}")
+    kc, vc = kvlib.copy(dev["key_cache"], dev["value_cache"], dev["block_mapping"])
+    torch.cuda.synchronize()
+    assert_caches(kc, vc, expected, f"copy {case.key}/{dtype}")
